@@ -1,0 +1,191 @@
+/*
+ * moe_mi355x.h -- C ABI of the MI355X (gfx950) MoE / QMoE library.
+ *
+ * The library implements the com.microsoft MoE and QMoE contrib ops (ONNX
+ * Runtime 1.26 op schemas, since-version 1) as hand-written HIP kernels.
+ * Everything here is plain C: pointers, sizes, enums and POD structs.  A HIP
+ * stream is passed as `void*` (hipStream_t), as ORT hands it to a plugin
+ * kernel through KernelContext::GetGPUComputeStream().
+ *
+ * Two layers are exported:
+ *
+ *   1. The op kernel (moe_kernel_*): what a Plugin-EP kernel registration
+ *      binds.  It replaces, one for one, the reference's kernel object:
+ *        moe_kernel_create   <- OpKernelBase<Derived>::CreateKernelImpl and the
+ *                               attribute-reading constructor
+ *                               (musa/ep/src/kernels/shared_inc/kernel_base.h:36-43,
+ *                                pattern musa/ep/src/kernels/llm/attention.cc:63-72,
+ *                                AttrOrDefault kernel_attributes.h:21-28)
+ *        moe_kernel_compute  <- OpKernelBase<Derived>::ComputeImpl -> Derived::Compute
+ *                               (kernel_base.h:45-84; attention.cc:100-256)
+ *        moe_kernel_release  <- OpKernelBase<Derived>::ReleaseImpl (kernel_base.h:86-89)
+ *      Inputs are given in the op's schema order (MoE: 8 inputs, QMoE: 11).
+ *
+ *   2. Stage launchers (moe_route_dispatch_launch): the device-launcher layer
+ *      below a kernel, following the reference convention of POD params +
+ *      device pointers + stream returning a runtime status
+ *      (musa/ep/src/kernels/math/topk_impl.h:10-33,
+ *       shared_inc/device_kernel_types.h:258-266).
+ *
+ * Status codes use OrtErrorCode numbering so a Plugin-EP shim can pass them to
+ * OrtApi::CreateStatus unchanged (the reference maps failures the same way:
+ * ORT_INVALID_ARGUMENT for bad attributes/shapes, ORT_NOT_IMPLEMENTED for an
+ * unsupported dtype/feature, ORT_EP_FAIL for runtime errors; e.g.
+ * musa/ep/src/kernels/math/topk.cc:143-187, attention.cc:101-158).
+ *
+ * Threading: a moe_kernel is immutable after creation; moe_kernel_compute may
+ * be called concurrently from several threads on different streams when each
+ * call passes its own workspace.  With workspace == NULL the kernel uses a
+ * workspace it caches per (device, stream), guarded by a mutex.
+ */
+#ifndef MOE_MI355X_H_
+#define MOE_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define MOE_API __attribute__((visibility("default")))
+#else
+#define MOE_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* OrtErrorCode numbering. */
+typedef enum moe_status {
+  MOE_OK = 0,
+  MOE_FAIL = 1,
+  MOE_INVALID_ARGUMENT = 2,
+  MOE_NOT_IMPLEMENTED = 9,
+  MOE_EP_FAIL = 11
+} moe_status;
+
+/* ONNX TensorProto element types, as the reference's MusaElementType
+ * (musa/ep/src/kernels/shared_inc/device_kernel_types.h:47-62). */
+typedef enum moe_elem_type {
+  MOE_ELEM_FLOAT = 1,
+  MOE_ELEM_UINT8 = 2,
+  MOE_ELEM_FLOAT16 = 10,
+  MOE_ELEM_BFLOAT16 = 16
+} moe_elem_type;
+
+typedef enum moe_activation {
+  MOE_ACT_RELU = 0,
+  MOE_ACT_GELU = 1,
+  MOE_ACT_SILU = 2,
+  MOE_ACT_IDENTITY = 3,
+  MOE_ACT_SWIGLU = 4
+} moe_activation;
+
+/* Node attributes of com.microsoft MoE / QMoE.  moe_attributes_init() fills
+ * the schema defaults; a shim sets each field it finds on the node. */
+typedef struct moe_attributes {
+  int64_t k;                         /* "k", default 1 */
+  int32_t activation_type;           /* "activation_type", moe_activation, default relu */
+  int32_t normalize_routing_weights; /* default 0 */
+  int32_t use_sparse_mixer;          /* default 0; nonzero -> MOE_NOT_IMPLEMENTED */
+  int32_t swiglu_fusion;             /* 0 unfused, 1 interleaved, 2 chunked; default 0 */
+  int32_t has_swiglu_limit;          /* "swiglu_limit" present? */
+  float swiglu_limit;
+  float activation_alpha;            /* default 1.0 */
+  float activation_beta;             /* default 0.0 */
+  int64_t expert_weight_bits;        /* QMoE only, default 4 */
+  int64_t block_size;                /* QMoE only, 0 = absent (per output channel) */
+  int32_t router_sigmoid;            /* library extension: sigmoid instead of softmax, default 0 */
+} moe_attributes;
+
+/* A tensor handed to the kernel.  data == NULL marks an absent optional
+ * input.  Device pointers (HBM); dims are row-major. */
+typedef struct moe_tensor {
+  const void *data;
+  int32_t elem_type; /* moe_elem_type */
+  int32_t rank;
+  int64_t dims[4];
+} moe_tensor;
+
+typedef struct moe_kernel moe_kernel;
+
+/* Fills `attrs` with the schema defaults of op_type ("MoE" or "QMoE"). */
+MOE_API moe_status moe_attributes_init(moe_attributes *attrs, const char *op_type);
+
+/* Parses the activation_type attribute string ("relu", "gelu", "silu",
+ * "identity", "swiglu"). */
+MOE_API moe_status moe_parse_activation(const char *name, int32_t *activation);
+
+/* Creates an immutable kernel for one node.  Validates the attributes. */
+MOE_API moe_status moe_kernel_create(const char *op_type, const moe_attributes *attrs,
+                             moe_kernel **out);
+
+/* Workspace bytes moe_kernel_compute needs for these inputs (shapes only are
+ * read).  Validates shapes and types. */
+MOE_API moe_status moe_kernel_workspace_size(const moe_kernel *kernel, const moe_tensor *inputs,
+                                     int32_t num_inputs, size_t *bytes);
+
+/* Runs the op: output is a device buffer of the input's shape and type.
+ * All work is enqueued on `stream`; no host synchronisation, no device->host
+ * reads.  workspace may be NULL (cached internal workspace). */
+MOE_API moe_status moe_kernel_compute(const moe_kernel *kernel, const moe_tensor *inputs,
+                              int32_t num_inputs, void *output, void *workspace,
+                              size_t workspace_bytes, void *stream);
+
+MOE_API void moe_kernel_release(moe_kernel *kernel);
+
+/* Byte offsets, inside a caller-provided workspace, of the routing results a
+ * moe_kernel_compute call leaves there (int32 topk_ids[T*k], float
+ * topk_w[T*k], int32 offsets[E+1], int32 perm[T*k], int32 inv_perm[T*k]).
+ * Library extension for parity tests; no reference counterpart. */
+typedef struct moe_workspace_layout {
+  size_t topk_ids, topk_w, offsets, perm, inv_perm, total;
+} moe_workspace_layout;
+MOE_API moe_status moe_kernel_workspace_layout(const moe_kernel *kernel, const moe_tensor *inputs,
+                                       int32_t num_inputs, moe_workspace_layout *out);
+
+/* Selects the expert-FFN kernel family: -1 automatic (default), 0 generic
+ * SIMT, 1 weight-streaming decode, 2 MFMA prefill.  A forced family that does
+ * not support a problem makes moe_kernel_compute return MOE_NOT_IMPLEMENTED.
+ * Library extension for tests and benchmarks; no reference counterpart.
+ * Call before the kernel is shared between threads. */
+MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
+
+/* Message of the last non-OK status returned on this thread. */
+MOE_API const char *moe_last_error(void);
+
+/* ------------------------------------------------------------------ */
+/* Stage launcher: router (softmax/sigmoid + top-k, ties -> lower expert id)
+ * and dispatch (per-expert histogram, exclusive scan, stable scatter).
+ * Device outputs:
+ *   topk_ids  [T*k] int32   expert of token t's j-th choice (j by descending logit)
+ *   topk_w    [T*k] float   routing weight
+ *   offsets   [E+1] int32   exclusive scan of per-expert counts (offsets[E] = T*k)
+ *   perm      [T*k] int32   row -> flat index t*k+j, expert-major, tokens ascending
+ *   inv_perm  [T*k] int32   flat index -> row
+ * scratch: moe_route_dispatch_scratch_size() bytes of device memory. */
+typedef struct moe_route_params {
+  const void *logits;
+  int32_t logits_type; /* moe_elem_type */
+  int32_t normalize;
+  int32_t sigmoid;
+  int32_t pad_;
+  int64_t num_tokens, num_experts, k;
+  int32_t *topk_ids;
+  float *topk_w;
+  int32_t *offsets;
+  int32_t *perm;
+  int32_t *inv_perm;
+  void *scratch;
+  size_t scratch_bytes;
+} moe_route_params;
+
+MOE_API size_t moe_route_dispatch_scratch_size(int64_t num_tokens, int64_t num_experts, int64_t k);
+MOE_API moe_status moe_route_dispatch_launch(const moe_route_params *params, void *stream);
+
+/* Library version string. */
+MOE_API const char *moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_MI355X_H_ */

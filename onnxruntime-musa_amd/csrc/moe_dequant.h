@@ -1,0 +1,167 @@
+// moe_dequant.h -- in-register dequantisation of QMoE weights into MFMA
+// operands (8 consecutive k of one weight row -> 8 x 16-bit in 4 dwords).
+//
+// Encoding (symmetric): int8 w = (q - 128) * s; int4 w = (nibble - 8) * s with
+// the even-k element in the low nibble of each byte.
+//
+// "Exact" converters produce the integer (q - zero_point) as fp16/bf16, which
+// is exact in both formats; the scale is then applied to fp32 MFMA partial
+// sums.  "Scaled" converters fold the scale in before the MFMA (one rounding
+// of (q - zp) * s to the 16-bit type), used where one MFMA's K range spans
+// several scale blocks.
+//
+// fp16 converters use the magic-exponent trick: 0x6400 | q is the fp16 value
+// 1024 + q for q < 1024, so one byte-permute/or builds two operands and one
+// packed subtract removes the bias.
+#pragma once
+
+#include "moe_device.h"
+
+namespace moe {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ half2_t bits_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// int4 dword (k0..k7) -> fp16 pairs of (nibble - 8), exact.
+__device__ __forceinline__ u32x4_t dq4_f16_exact(uint32_t v) {
+  const uint32_t t = v & 0x0F0F0F0Fu;         // even k nibbles, one per byte
+  const uint32_t u = (v >> 4) & 0x0F0F0F0Fu;  // odd k nibbles
+  const half2_t bias = {static_cast<_Float16>(1032.0f), static_cast<_Float16>(1032.0f)};
+  u32x4_t r;
+  r[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c040c00u) | 0x64006400u) - bias);
+  r[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c050c01u) | 0x64006400u) - bias);
+  r[2] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c060c02u) | 0x64006400u) - bias);
+  r[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c070c03u) | 0x64006400u) - bias);
+  return r;
+}
+
+// int8 dwords (k0..k3, k4..k7) -> fp16 pairs of (q - 128), exact.
+__device__ __forceinline__ u32x4_t dq8_f16_exact(uint32_t v0, uint32_t v1) {
+  const uint32_t c = 0x64646464u;
+  const half2_t bias = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+  u32x4_t r;
+  r[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, v0, 0x04010400u)) - bias);
+  r[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, v0, 0x04030402u)) - bias);
+  r[2] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, v1, 0x04010400u)) - bias);
+  r[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, v1, 0x04030402u)) - bias);
+  return r;
+}
+
+// Packs the bf16 images of two fp32 values whose low 16 bits are zero (small
+// integers), lo in bits 0-15.
+__device__ __forceinline__ uint32_t pack_bf16_exact(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+__device__ __forceinline__ u32x4_t dq4_bf16_exact(uint32_t v) {
+  u32x4_t r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (v >> (8 * b)) & 0xFFu;
+    const float lo = static_cast<float>(byte & 0xFu) - 8.0f;
+    const float hi = static_cast<float>(byte >> 4) - 8.0f;
+    r[b] = pack_bf16_exact(lo, hi);
+  }
+  return r;
+}
+
+__device__ __forceinline__ u32x4_t dq8_bf16_exact(uint32_t v0, uint32_t v1) {
+  u32x4_t r;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    r[b] = pack_bf16_exact(static_cast<float>((v0 >> (16 * b)) & 0xFFu) - 128.0f,
+                           static_cast<float>((v0 >> (16 * b + 8)) & 0xFFu) - 128.0f);
+    r[2 + b] = pack_bf16_exact(static_cast<float>((v1 >> (16 * b)) & 0xFFu) - 128.0f,
+                               static_cast<float>((v1 >> (16 * b + 8)) & 0xFFu) - 128.0f);
+  }
+  return r;
+}
+
+// Rounds two fp32 values to the 16-bit activation type and packs them.
+template <typename AT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  const half2_t h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+  return h2_bits(h);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// Scaled converters: 8 weights times per-element-group scale s -> 16-bit.
+template <typename AT>
+__device__ __forceinline__ u32x4_t dq4_scaled(uint32_t v, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (v >> (8 * b)) & 0xFFu;
+    r[b] = pack2<AT>((static_cast<float>(byte & 0xFu) - 8.0f) * s,
+                     (static_cast<float>(byte >> 4) - 8.0f) * s);
+  }
+  return r;
+}
+
+template <typename AT>
+__device__ __forceinline__ u32x4_t dq8_scaled(uint32_t v0, uint32_t v1, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    r[b] = pack2<AT>((static_cast<float>((v0 >> (16 * b)) & 0xFFu) - 128.0f) * s,
+                     (static_cast<float>((v0 >> (16 * b + 8)) & 0xFFu) - 128.0f) * s);
+    r[2 + b] = pack2<AT>((static_cast<float>((v1 >> (16 * b)) & 0xFFu) - 128.0f) * s,
+                         (static_cast<float>((v1 >> (16 * b + 8)) & 0xFFu) - 128.0f) * s);
+  }
+  return r;
+}
+
+template <typename AT>
+__device__ __forceinline__ u32x4_t dq4_exact(uint32_t v);
+template <>
+__device__ __forceinline__ u32x4_t dq4_exact<F16>(uint32_t v) { return dq4_f16_exact(v); }
+template <>
+__device__ __forceinline__ u32x4_t dq4_exact<BF16>(uint32_t v) { return dq4_bf16_exact(v); }
+
+template <typename AT>
+__device__ __forceinline__ u32x4_t dq8_exact(uint32_t v0, uint32_t v1);
+template <>
+__device__ __forceinline__ u32x4_t dq8_exact<F16>(uint32_t v0, uint32_t v1) {
+  return dq8_f16_exact(v0, v1);
+}
+template <>
+__device__ __forceinline__ u32x4_t dq8_exact<BF16>(uint32_t v0, uint32_t v1) {
+  return dq8_bf16_exact(v0, v1);
+}
+
+// 16x16x32 MFMA on 8 x 16-bit operands held as 4 dwords.
+template <typename AT>
+__device__ __forceinline__ floatx4_t mfma16x16x32(u32x4_t a, u32x4_t b, floatx4_t c);
+template <>
+__device__ __forceinline__ floatx4_t mfma16x16x32<F16>(u32x4_t a, u32x4_t b, floatx4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx4_t mfma16x16x32<BF16>(u32x4_t a, u32x4_t b, floatx4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// 32x32x16 MFMA.
+template <typename AT>
+__device__ __forceinline__ floatx16_t mfma32x32x16(u32x4_t a, u32x4_t b, floatx16_t c);
+template <>
+__device__ __forceinline__ floatx16_t mfma32x32x16<F16>(u32x4_t a, u32x4_t b, floatx16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
+                                                __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx16_t mfma32x32x16<BF16>(u32x4_t a, u32x4_t b, floatx16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+}  // namespace moe

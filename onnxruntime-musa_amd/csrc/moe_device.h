@@ -1,0 +1,107 @@
+// moe_device.h -- device helpers shared by the gfx950 MoE kernels.
+//
+// Activations are fp32, fp16 (_Float16) or bf16 (raw uint16_t bits; bf16 <->
+// fp32 conversion is done on bits, round-to-nearest-even, the same rounding as
+// the reference's float32_to_bfloat16_bits, test/ops/op_test_utils.py:235-245).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kWave = 64;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// Element tags.
+struct F32 { using storage = float; static constexpr int kId = 1; };
+struct F16 { using storage = _Float16; static constexpr int kId = 10; };
+struct BF16 { using storage = uint16_t; static constexpr int kId = 16; };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
+  x += 0x7FFFu + ((x >> 16) & 1u);
+  return static_cast<uint16_t>(x >> 16);
+}
+
+template <typename Tag>
+__device__ __forceinline__ float to_f32(typename Tag::storage v);
+template <>
+__device__ __forceinline__ float to_f32<F32>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<F16>(_Float16 v) { return static_cast<float>(v); }
+template <>
+__device__ __forceinline__ float to_f32<BF16>(uint16_t v) { return bf16_to_f32(v); }
+
+template <typename Tag>
+__device__ __forceinline__ typename Tag::storage from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<F32>(float v) { return v; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<F16>(float v) { return static_cast<_Float16>(v); }
+template <>
+__device__ __forceinline__ uint16_t from_f32<BF16>(float v) { return f32_to_bf16(v); }
+
+// Load one element of a runtime-typed buffer (scales, biases) as fp32.
+__device__ __forceinline__ float load_any(const void* p, int elem_type, int64_t i) {
+  if (elem_type == 1) return static_cast<const float*>(p)[i];
+  if (elem_type == 10) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// ---- wave reductions (64 lanes, butterfly over __shfl_xor) ----
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// ---- activations (fp32) ----
+enum Act : int { kRelu = 0, kGelu = 1, kSilu = 2, kIdentity = 3, kSwiglu = 4 };
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float act_single(float x, int act) {
+  switch (act) {
+    case kRelu: return x > 0.0f ? x : 0.0f;
+    case kGelu: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+    case kSilu: return x * sigmoid_f(x);
+    default: return x;
+  }
+}
+
+// SwiGLU with clamp: G = min(g, limit), L = clamp(l, -limit, limit),
+// out = G * sigmoid(alpha * G) * (L + beta).
+__device__ __forceinline__ float swiglu_f(float g, float l, float alpha, float beta,
+                                          float limit) {
+  g = fminf(g, limit);
+  l = fminf(fmaxf(l, -limit), limit);
+  return g * sigmoid_f(alpha * g) * (l + beta);
+}
+
+// Combines a gate value and (if gated) a linear value into one activation.
+// gated == false: act(g).  activation == swiglu: swiglu(g, l).  Otherwise
+// act(g) * l (fc3 gating).
+__device__ __forceinline__ float apply_act(float g, float l, bool gated, int act, float alpha,
+                                           float beta, float limit) {
+  if (!gated) return act_single(g, act);
+  if (act == kSwiglu) return swiglu_f(g, l, alpha, beta, limit);
+  return act_single(g, act) * l;
+}
+
+}  // namespace moe

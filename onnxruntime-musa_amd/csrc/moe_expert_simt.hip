@@ -1,0 +1,157 @@
+// moe_expert_simt.hip -- generic expert FFN kernels (any activation dtype,
+// any weight format) and the finalize gather-reduce.
+//
+// These serve the fp32 activation path (the small fp32 MoE config: fp32
+// accumulation, max-abs 1e-4 against the oracle) and are the functional
+// fallback for shapes the MFMA paths do not cover.  One wavefront computes one
+// output feature of one dispatched row: lanes stride over K with coalesced
+// loads, each lane accumulates in fp32, a butterfly sum reduces the wave.
+#include "moe_device.h"
+#include "moe_launch.h"
+
+namespace moe {
+namespace {
+
+// fp32 value of element (n, kk) of expert e's [N, K] weight matrix.
+struct WeightView {
+  const void* w;
+  const void* s;
+  int32_t wfmt, act_type, scale_type;
+  int64_t N, K, block_size;
+
+  __device__ __forceinline__ float get(int64_t e, int64_t n, int64_t kk) const {
+    if (wfmt == kDense) return load_any(w, act_type, (e * N + n) * K + kk);
+    const uint8_t* q = static_cast<const uint8_t*>(w);
+    const int64_t nblk = block_size > 0 ? K / block_size : 1;
+    const float sc =
+        load_any(s, scale_type, (e * N + n) * nblk + (block_size > 0 ? kk / block_size : 0));
+    int v;
+    if (wfmt == kInt8) {
+      v = static_cast<int>(q[(e * N + n) * K + kk]) - 128;
+    } else {
+      const uint8_t b = q[(e * N + n) * (K / 2) + (kk >> 1)];
+      v = static_cast<int>((kk & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+    }
+    return static_cast<float>(v) * sc;
+  }
+};
+
+__device__ __forceinline__ float load_act(const void* p, int t, int64_t i) {
+  return load_any(p, t, i);
+}
+
+// fc1 (+fc3) + bias + activation: act[r, i].
+__global__ void __launch_bounds__(256) fc1_simt_kernel(ExpertArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t i = static_cast<int64_t>(blockIdx.y) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int64_t r = blockIdx.x;
+  if (i >= a.I) return;
+  const int32_t f = a.perm[r];
+  const int64_t tok = f / a.k;
+  const int64_t e = a.topk_ids[f];
+  const bool gated = a.gate_mode != kGateNone;
+  const int64_t N1 = (a.gate_mode == kGateInterleaved || a.gate_mode == kGateChunked) ? 2 * a.I : a.I;
+  int64_t ng = i, nl = 0;
+  if (a.gate_mode == kGateInterleaved) { ng = 2 * i; nl = 2 * i + 1; }
+  else if (a.gate_mode == kGateChunked) { ng = i; nl = a.I + i; }
+  else if (a.gate_mode == kGateFc3) { ng = i; nl = i; }
+  const WeightView w1{a.w1, a.s1, a.wfmt, a.act_type, a.scale_type, N1, a.H, a.block_size};
+  const WeightView w3{a.w3, a.s3, a.wfmt, a.act_type, a.scale_type, a.I, a.H, a.block_size};
+  float sg = 0.0f, sl = 0.0f;
+  for (int64_t kk = lane; kk < a.H; kk += kWave) {
+    const float xv = load_act(a.x, a.act_type, tok * a.H + kk);
+    sg += xv * w1.get(e, ng, kk);
+    if (a.gate_mode == kGateFc3) sl += xv * w3.get(e, nl, kk);
+    else if (gated) sl += xv * w1.get(e, nl, kk);
+  }
+  sg = wave_sum(sg);
+  sl = wave_sum(sl);
+  if (lane == 0) {
+    if (a.b1) sg += load_any(a.b1, a.act_type, e * N1 + ng);
+    if (a.gate_mode == kGateFc3) {
+      if (a.b3) sl += load_any(a.b3, a.act_type, e * a.I + nl);
+    } else if (gated && a.b1) {
+      sl += load_any(a.b1, a.act_type, e * N1 + nl);
+    }
+    const float v = apply_act(sg, sl, gated, a.activation, a.alpha, a.beta, a.limit);
+    const int64_t o = r * a.I + i;
+    if (a.act_type == MOE_ELEM_FLOAT) static_cast<float*>(a.act)[o] = v;
+    else if (a.act_type == MOE_ELEM_FLOAT16) static_cast<_Float16*>(a.act)[o] = static_cast<_Float16>(v);
+    else static_cast<uint16_t*>(a.act)[o] = f32_to_bf16(v);
+  }
+}
+
+// fc2 + bias: y2[r, h] (fp32).
+__global__ void __launch_bounds__(256) fc2_simt_kernel(ExpertArgs a) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t h = static_cast<int64_t>(blockIdx.y) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  const int64_t r = blockIdx.x;
+  if (h >= a.H) return;
+  const int64_t e = a.topk_ids[a.perm[r]];
+  const WeightView w2{a.w2, a.s2, a.wfmt, a.act_type, a.scale_type, a.H, a.I, a.block_size};
+  float s = 0.0f;
+  for (int64_t kk = lane; kk < a.I; kk += kWave)
+    s += load_act(a.act, a.act_type, r * a.I + kk) * w2.get(e, h, kk);
+  s = wave_sum(s);
+  if (lane == 0) {
+    if (a.b2) s += load_any(a.b2, a.act_type, e * a.H + h);
+    a.y2[r * a.H + h] = s;
+  }
+}
+
+// out[t, h] = sum_j w[t, j] * y2[inv_perm[t*k + j], h], summed in slot order.
+template <typename OT>
+__global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
+  const int64_t t = blockIdx.x;
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x) * 4;
+  if (h0 >= a.H) return;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t j = 0; j < a.k; ++j) {
+    const int64_t f = t * a.k + j;
+    const float w = a.topk_w[f];
+    const float* y = a.y2 + static_cast<int64_t>(a.inv_perm[f]) * a.H;
+    if (h0 + 4 <= a.H && (a.H % 4) == 0) {
+      const float4 v = *reinterpret_cast<const float4*>(y + h0);
+      acc[0] += w * v.x;
+      acc[1] += w * v.y;
+      acc[2] += w * v.z;
+      acc[3] += w * v.w;
+    } else {
+      for (int c = 0; c < 4 && h0 + c < a.H; ++c) acc[c] += w * y[h0 + c];
+    }
+  }
+  typename OT::storage* out = static_cast<typename OT::storage*>(a.out);
+  for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
+}
+
+}  // namespace
+
+hipError_t launch_fc1_simt(const ExpertArgs& a, hipStream_t stream) {
+  const int64_t rows = a.T * a.k;
+  if (rows == 0) return hipSuccess;
+  dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((a.I + 3) / 4));
+  hipLaunchKernelGGL(fc1_simt_kernel, grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream) {
+  const int64_t rows = a.T * a.k;
+  if (rows == 0) return hipSuccess;
+  dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((a.H + 3) / 4));
+  hipLaunchKernelGGL(fc2_simt_kernel, grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream) {
+  if (a.T == 0) return hipSuccess;
+  dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + 1023) / 1024));
+  switch (a.act_type) {
+    case MOE_ELEM_FLOAT: hipLaunchKernelGGL(finalize_kernel<F32>, grid, dim3(256), 0, stream, a); break;
+    case MOE_ELEM_FLOAT16: hipLaunchKernelGGL(finalize_kernel<F16>, grid, dim3(256), 0, stream, a); break;
+    case MOE_ELEM_BFLOAT16: hipLaunchKernelGGL(finalize_kernel<BF16>, grid, dim3(256), 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace moe

@@ -1,0 +1,88 @@
+// moe_launch.h -- internal launcher interface between the host op and the
+// gfx950 kernels.  POD argument structs + stream, returning hipError_t, the
+// reference's device-launcher convention (musa/ep/src/kernels/math/topk_impl.h:10-33).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "moe_mi355x.h"
+
+namespace moe {
+
+enum WeightFormat : int { kDense = 0, kInt4 = 4, kInt8 = 8 };
+
+// How the activation input pairs are laid out in the fc1 output.
+enum GateMode : int {
+  kGateNone = 0,         // a = act(fc1)
+  kGateFc3 = 1,          // gate = fc1 row i, linear = fc3 row i
+  kGateInterleaved = 2,  // fused fc1 [2I]: gate = row 2i, linear = row 2i+1
+  kGateChunked = 3       // fused fc1 [2I]: gate = row i, linear = row I+i
+};
+
+enum ExpertPath : int { kPathSimt = 0, kPathDecode = 1, kPathPrefill = 2 };
+
+// Maximum router width handled by the wave-per-token router (8 values per lane).
+constexpr int64_t kMaxExperts = 512;
+constexpr int64_t kMaxTopK = 64;
+// Token count up to which routing + dispatch runs as one single-workgroup kernel.
+constexpr int64_t kSmallRouteTokens = 256;
+// Tokens routed per workgroup in the multi-workgroup router.
+constexpr int kRouteTokensPerBlock = 64;
+
+struct RouteArgs {
+  moe_route_params p;
+  int32_t* tile_offsets;  // optional [E+1]: prefix of ceil(count_e / tile_m)
+  int32_t tile_m;
+};
+
+size_t route_scratch_bytes(int64_t T, int64_t E, int64_t k);
+hipError_t launch_route_dispatch(const RouteArgs& a, hipStream_t stream);
+
+struct ExpertArgs {
+  int64_t T, H, I, E, k;
+  int32_t act_type;    // moe_elem_type of input/output/bias
+  int32_t wfmt;        // WeightFormat
+  int32_t scale_type;  // moe_elem_type of scales (quantized only)
+  int64_t block_size;  // 0 = one scale per output channel
+  int32_t activation;  // moe_activation
+  int32_t gate_mode;   // GateMode
+  float alpha, beta, limit;
+  // routing (device)
+  const int32_t* offsets;       // [E+1]
+  const int32_t* perm;          // [T*k]
+  const int32_t* inv_perm;      // [T*k]
+  const int32_t* topk_ids;      // [T*k]
+  const float* topk_w;          // [T*k]
+  const int32_t* tile_offsets;  // [E+1], prefill path
+  // fc1 / fc3
+  const void* x;  // [T, H]
+  const void *w1, *s1, *b1;
+  const void *w3, *s3, *b3;
+  // fc2
+  const void *w2, *s2, *b2;
+  // intermediates
+  void* act;   // [T*k, I] in act_type
+  float* y2;   // [T*k, H] fp32
+  void* out;   // [T, H] act_type
+};
+
+hipError_t launch_fc1_simt(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc2_decode(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc2_prefill(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
+
+// Whether the MFMA paths accept this problem (fp16/bf16 activations, K a
+// multiple of 32, block sizes the dequant loaders handle).
+bool decode_supported(const ExpertArgs& a);
+bool prefill_supported(const ExpertArgs& a);
+
+// Row tile of the prefill grouped GEMM (rows of one expert per workgroup).
+constexpr int kPrefillTileM = 128;
+// Largest token count served by the decode (weight-streaming) path.
+constexpr int64_t kDecodeMaxTokens = 64;
+
+}  // namespace moe

@@ -1,0 +1,528 @@
+// moe_op.cc -- host side of the com.microsoft MoE / QMoE kernels (C++20).
+//
+// Mirrors the reference's op-kernel structure: attributes are read once at
+// creation and the kernel is immutable afterwards (ctor pattern
+// musa/ep/src/kernels/llm/attention.cc:63-72); Compute validates inputs,
+// plans scratch and enqueues device launches on the caller's stream with no
+// host synchronisation (attention.cc:100-256, scratch pattern :29-61).
+// Errors never cross the ABI as exceptions: every entry point returns a
+// status (the reference wraps entries in EXCEPTION_TO_RETURNED_STATUS_*,
+// musa/ep/src/plugin_ep_utils.h:92-106).
+//
+// Input contract (op schemas of ONNX Runtime 1.26, com.microsoft, since 1):
+//   MoE : input, router_probs, fc1_experts_weights, fc1_experts_bias?,
+//         fc2_experts_weights, fc2_experts_bias?, fc3_experts_weights?,
+//         fc3_experts_bias?
+//   QMoE: input, router_probs, fc1_experts_weights, fc1_scales,
+//         fc1_experts_bias?, fc2_experts_weights, fc2_scales,
+//         fc2_experts_bias?, fc3_experts_weights?, fc3_scales?,
+//         fc3_experts_bias?
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <exception>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <new>
+#include <string>
+#include <utility>
+
+#include "moe_launch.h"
+#include "moe_mi355x.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+moe_status fail(moe_status code, std::string msg) {
+  g_last_error = std::move(msg);
+  return code;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool is_float_type(int32_t t) {
+  return t == MOE_ELEM_FLOAT || t == MOE_ELEM_FLOAT16 || t == MOE_ELEM_BFLOAT16;
+}
+size_t elem_size(int32_t t) { return t == MOE_ELEM_FLOAT ? 4 : (t == MOE_ELEM_UINT8 ? 1 : 2); }
+
+std::string dims_str(const moe_tensor& t) {
+  std::string s = "[";
+  for (int i = 0; i < t.rank; ++i) s += (i ? "," : "") + std::to_string(t.dims[i]);
+  return s + "]";
+}
+
+// Shapes and pointers of one call, validated.
+struct Problem {
+  int64_t T = 0, H = 0, I = 0, E = 0, k = 0, N1 = 0;
+  int32_t act_type = 0, scale_type = MOE_ELEM_FLOAT16, wfmt = moe::kDense, gate_mode = moe::kGateNone;
+  int64_t block_size = 0;
+  const moe_tensor* in[11] = {};
+};
+
+// Workspace sections, byte offsets from the workspace base.
+struct Layout {
+  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, total;
+  size_t route_scratch_bytes;
+};
+
+Layout plan_layout(const Problem& p) {
+  Layout l{};
+  const size_t rows = static_cast<size_t>(p.T * p.k);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes);
+    return at;
+  };
+  l.topk_ids = take(rows * 4);
+  l.topk_w = take(rows * 4);
+  l.offsets = take(static_cast<size_t>(p.E + 1) * 4);
+  l.tile_offsets = take(static_cast<size_t>(p.E + 1) * 4);
+  l.perm = take(rows * 4);
+  l.inv_perm = take(rows * 4);
+  l.route_scratch_bytes = moe::route_scratch_bytes(p.T, p.E, p.k);
+  l.route_scratch = take(l.route_scratch_bytes);
+  l.act = take(rows * static_cast<size_t>(p.I) * elem_size(p.act_type));
+  l.y2 = take(rows * static_cast<size_t>(p.H) * 4);
+  l.total = o;
+  return l;
+}
+
+}  // namespace
+
+struct moe_kernel {
+  bool quantized = false;
+  moe_attributes attrs{};
+  int32_t forced_path = -1;
+  std::mutex mu;
+  std::map<std::pair<int, void*>, std::pair<void*, size_t>> ws_cache;  // (device, stream) -> buffer
+
+  ~moe_kernel() {
+    for (auto& kv : ws_cache)
+      if (kv.second.first) (void)hipFree(kv.second.first);
+  }
+};
+
+namespace {
+
+moe_status validate(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, Problem* out) {
+  Problem p;
+  const bool q = kr->quantized;
+  const int32_t need = q ? 7 : 5;
+  const int32_t max_in = q ? 11 : 8;
+  if (!inputs || n < need)
+    return fail(MOE_INVALID_ARGUMENT, std::string(q ? "QMoE" : "MoE") + " expects at least " +
+                                          std::to_string(need) + " inputs, got " + std::to_string(n));
+  if (n > max_in) {
+    for (int32_t i = max_in; i < n; ++i)
+      if (inputs[i].data)
+        return fail(MOE_NOT_IMPLEMENTED,
+                    "input " + std::to_string(i) + " (zero points) is not supported");
+    n = max_in;
+  }
+  for (int32_t i = 0; i < n; ++i) p.in[i] = inputs[i].data ? &inputs[i] : nullptr;
+  const moe_tensor *x = p.in[0], *router = p.in[1], *w1 = p.in[2];
+  const moe_tensor *s1 = q ? p.in[3] : nullptr, *b1 = q ? p.in[4] : p.in[3];
+  const moe_tensor *w2 = q ? p.in[5] : p.in[4], *s2 = q ? p.in[6] : nullptr;
+  const moe_tensor *b2 = q ? p.in[7] : p.in[5];
+  const moe_tensor *w3 = q ? (n > 8 ? p.in[8] : nullptr) : (n > 6 ? p.in[6] : nullptr);
+  const moe_tensor *s3 = q ? (n > 9 ? p.in[9] : nullptr) : nullptr;
+  const moe_tensor *b3 = q ? (n > 10 ? p.in[10] : nullptr) : (n > 7 ? p.in[7] : nullptr);
+  if (!x || !router || !w1 || !w2) return fail(MOE_INVALID_ARGUMENT, "missing required input");
+  if (q && (!s1 || !s2)) return fail(MOE_INVALID_ARGUMENT, "QMoE requires fc1_scales and fc2_scales");
+
+  // input [T, H] or [B, S, H]
+  if (x->rank != 2 && x->rank != 3)
+    return fail(MOE_INVALID_ARGUMENT, "input must be 2D or 3D, got " + dims_str(*x));
+  p.H = x->dims[x->rank - 1];
+  p.T = x->dims[0] * (x->rank == 3 ? x->dims[1] : 1);
+  p.act_type = x->elem_type;
+  if (!is_float_type(p.act_type))
+    return fail(MOE_NOT_IMPLEMENTED, "input type must be float, float16 or bfloat16");
+  if (router->elem_type != p.act_type)
+    return fail(MOE_INVALID_ARGUMENT, "router_probs must have the input's type");
+  if (router->rank != 2 || router->dims[0] != p.T)
+    return fail(MOE_INVALID_ARGUMENT, "router_probs must be [num_tokens, num_experts], got " + dims_str(*router));
+  p.E = router->dims[1];
+  if (p.E <= 0) return fail(MOE_INVALID_ARGUMENT, "num_experts must be positive");
+  if (p.E > moe::kMaxExperts)
+    return fail(MOE_NOT_IMPLEMENTED, "num_experts > " + std::to_string(moe::kMaxExperts));
+
+  const moe_attributes& at = kr->attrs;
+  p.k = at.k;
+  if (p.k < 1 || p.k > p.E)
+    return fail(MOE_INVALID_ARGUMENT, "k must be in [1, num_experts], got " + std::to_string(p.k));
+  if (p.k > moe::kMaxTopK) return fail(MOE_NOT_IMPLEMENTED, "k > 64 is not supported");
+
+  int64_t pack = 1;
+  if (q) {
+    pack = at.expert_weight_bits == 4 ? 2 : 1;
+    p.wfmt = at.expert_weight_bits == 4 ? moe::kInt4 : moe::kInt8;
+    if (w1->elem_type != MOE_ELEM_UINT8 || w2->elem_type != MOE_ELEM_UINT8 ||
+        (w3 && w3->elem_type != MOE_ELEM_UINT8))
+      return fail(MOE_INVALID_ARGUMENT, "QMoE expert weights must be uint8");
+    p.scale_type = s1->elem_type;
+    if (!is_float_type(p.scale_type) || s2->elem_type != p.scale_type ||
+        (s3 && s3->elem_type != p.scale_type))
+      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must share one float type");
+    p.block_size = at.block_size;
+  } else {
+    if (w1->elem_type != p.act_type || w2->elem_type != p.act_type ||
+        (w3 && w3->elem_type != p.act_type))
+      return fail(MOE_INVALID_ARGUMENT, "MoE expert weights must have the input's type");
+  }
+  if (w1->rank != 3 || w2->rank != 3)
+    return fail(MOE_INVALID_ARGUMENT, "expert weights must be 3D");
+  if (w1->dims[0] != p.E || w2->dims[0] != p.E)
+    return fail(MOE_INVALID_ARGUMENT, "expert weight dim 0 must equal num_experts");
+  if (w1->dims[2] * pack != p.H)
+    return fail(MOE_INVALID_ARGUMENT, "fc1_experts_weights " + dims_str(*w1) + " does not match hidden_size " +
+                                          std::to_string(p.H));
+  if (w2->dims[1] != p.H)
+    return fail(MOE_INVALID_ARGUMENT, "fc2_experts_weights " + dims_str(*w2) + " does not match hidden_size");
+  p.I = w2->dims[2] * pack;
+  if (p.I <= 0 || p.H <= 0) return fail(MOE_INVALID_ARGUMENT, "hidden and inter sizes must be positive");
+
+  const bool swiglu = at.activation_type == MOE_ACT_SWIGLU;
+  if (w3) {
+    if (swiglu && at.swiglu_fusion != 0)
+      return fail(MOE_INVALID_ARGUMENT, "fc3 weights require swiglu_fusion = 0");
+    p.gate_mode = moe::kGateFc3;
+    p.N1 = p.I;
+    if (w3->rank != 3 || w3->dims[0] != p.E || w3->dims[1] != p.I || w3->dims[2] * pack != p.H)
+      return fail(MOE_INVALID_ARGUMENT, "fc3_experts_weights must be [E, inter, hidden/pack], got " + dims_str(*w3));
+    if (q && !s3) return fail(MOE_INVALID_ARGUMENT, "fc3_scales required with fc3_experts_weights");
+  } else if (swiglu) {
+    if (at.swiglu_fusion == 1) p.gate_mode = moe::kGateInterleaved;
+    else if (at.swiglu_fusion == 2) p.gate_mode = moe::kGateChunked;
+    else
+      return fail(MOE_NOT_IMPLEMENTED,
+                  "swiglu without fc3 needs fused fc1 weights (swiglu_fusion 1 or 2)");
+    p.N1 = 2 * p.I;
+  } else {
+    p.N1 = p.I;
+  }
+  if (w1->dims[1] != p.N1)
+    return fail(MOE_INVALID_ARGUMENT, "fc1_experts_weights dim 1 must be " + std::to_string(p.N1) + ", got " +
+                                          dims_str(*w1));
+  auto check_bias = [&](const moe_tensor* b, int64_t N, const char* name) -> moe_status {
+    if (!b) return MOE_OK;
+    if (b->elem_type != p.act_type || b->rank != 2 || b->dims[0] != p.E || b->dims[1] != N)
+      return fail(MOE_INVALID_ARGUMENT, std::string(name) + " must be [" + std::to_string(p.E) + ", " +
+                                            std::to_string(N) + "] of the input's type, got " + dims_str(*b));
+    return MOE_OK;
+  };
+  moe_status st;
+  if ((st = check_bias(b1, p.N1, "fc1_experts_bias")) != MOE_OK) return st;
+  if ((st = check_bias(b2, p.H, "fc2_experts_bias")) != MOE_OK) return st;
+  if ((st = check_bias(b3, p.I, "fc3_experts_bias")) != MOE_OK) return st;
+
+  if (q) {
+    const int64_t bs = p.block_size;
+    if (bs > 0) {
+      if (bs < 16 || (bs & (bs - 1)))
+        return fail(MOE_INVALID_ARGUMENT, "block_size must be a power of two >= 16, got " + std::to_string(bs));
+      if (p.H % bs || p.I % bs)
+        return fail(MOE_INVALID_ARGUMENT, "block_size must divide hidden_size and inter_size");
+    }
+    auto check_scale = [&](const moe_tensor* s, int64_t N, int64_t K, const char* name) -> moe_status {
+      const bool ok = bs > 0 ? (s->rank == 3 && s->dims[0] == p.E && s->dims[1] == N && s->dims[2] == K / bs)
+                             : (s->rank == 2 && s->dims[0] == p.E && s->dims[1] == N);
+      if (!ok)
+        return fail(MOE_INVALID_ARGUMENT, std::string(name) + " has shape " + dims_str(*s) +
+                                              (bs > 0 ? ", expected [E, N, K/block_size]" : ", expected [E, N]"));
+      return MOE_OK;
+    };
+    if ((st = check_scale(s1, p.N1, p.H, "fc1_scales")) != MOE_OK) return st;
+    if ((st = check_scale(s2, p.H, p.I, "fc2_scales")) != MOE_OK) return st;
+    if (w3 && (st = check_scale(s3, p.I, p.H, "fc3_scales")) != MOE_OK) return st;
+  }
+  if (p.T * p.k > std::numeric_limits<int32_t>::max() / 2)
+    return fail(MOE_NOT_IMPLEMENTED, "num_tokens * k exceeds the int32 row index range");
+  *out = p;
+  return MOE_OK;
+}
+
+moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout& l, uint8_t* ws,
+                            void* output) {
+  const bool q = kr->quantized;
+  moe::ExpertArgs a{};
+  a.T = p.T; a.H = p.H; a.I = p.I; a.E = p.E; a.k = p.k;
+  a.act_type = p.act_type;
+  a.wfmt = p.wfmt;
+  a.scale_type = p.scale_type;
+  a.block_size = p.block_size;
+  a.activation = kr->attrs.activation_type;
+  a.gate_mode = p.gate_mode;
+  a.alpha = kr->attrs.activation_alpha;
+  a.beta = kr->attrs.activation_beta;
+  a.limit = kr->attrs.has_swiglu_limit ? kr->attrs.swiglu_limit : std::numeric_limits<float>::infinity();
+  a.offsets = reinterpret_cast<const int32_t*>(ws + l.offsets);
+  a.perm = reinterpret_cast<const int32_t*>(ws + l.perm);
+  a.inv_perm = reinterpret_cast<const int32_t*>(ws + l.inv_perm);
+  a.topk_ids = reinterpret_cast<const int32_t*>(ws + l.topk_ids);
+  a.topk_w = reinterpret_cast<const float*>(ws + l.topk_w);
+  a.tile_offsets = reinterpret_cast<const int32_t*>(ws + l.tile_offsets);
+  auto d = [&](int i) -> const void* { return p.in[i] ? p.in[i]->data : nullptr; };
+  a.x = d(0);
+  a.w1 = d(2);
+  if (q) {
+    a.s1 = d(3); a.b1 = d(4); a.w2 = d(5); a.s2 = d(6); a.b2 = d(7);
+    a.w3 = d(8); a.s3 = d(9); a.b3 = d(10);
+  } else {
+    a.b1 = d(3); a.w2 = d(4); a.b2 = d(5); a.w3 = d(6); a.b3 = d(7);
+  }
+  a.act = ws + l.act;
+  a.y2 = reinterpret_cast<float*>(ws + l.y2);
+  a.out = output;
+  return a;
+}
+
+int choose_path(const moe_kernel* kr, const moe::ExpertArgs& a) {
+  const int forced = kr->forced_path;
+  if (forced == moe::kPathSimt) return moe::kPathSimt;
+  if (forced == moe::kPathDecode && moe::decode_supported(a)) return moe::kPathDecode;
+  if (forced == moe::kPathPrefill && moe::prefill_supported(a)) return moe::kPathPrefill;
+  if (forced >= 0) return -1;
+  if (moe::decode_supported(a)) return moe::kPathDecode;
+  if (moe::prefill_supported(a)) return moe::kPathPrefill;
+  return moe::kPathSimt;
+}
+
+moe_status hip_fail(hipError_t e, const char* what) {
+  return fail(MOE_EP_FAIL, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+moe_status moe_attributes_init(moe_attributes* a, const char* op_type) {
+  if (!a || !op_type) return fail(MOE_INVALID_ARGUMENT, "null argument");
+  const bool q = std::strcmp(op_type, "QMoE") == 0;
+  if (!q && std::strcmp(op_type, "MoE") != 0)
+    return fail(MOE_INVALID_ARGUMENT, std::string("unknown op type ") + op_type);
+  *a = moe_attributes{};
+  a->k = 1;
+  a->activation_type = MOE_ACT_RELU;
+  a->normalize_routing_weights = 0;
+  a->use_sparse_mixer = 0;
+  a->swiglu_fusion = 0;
+  a->has_swiglu_limit = 0;
+  a->swiglu_limit = std::numeric_limits<float>::infinity();
+  a->activation_alpha = 1.0f;
+  a->activation_beta = 0.0f;
+  a->expert_weight_bits = q ? 4 : 0;
+  a->block_size = 0;
+  a->router_sigmoid = 0;
+  return MOE_OK;
+}
+
+moe_status moe_parse_activation(const char* name, int32_t* act) {
+  if (!name || !act) return fail(MOE_INVALID_ARGUMENT, "null argument");
+  static const std::pair<const char*, int32_t> kNames[] = {
+      {"relu", MOE_ACT_RELU}, {"gelu", MOE_ACT_GELU}, {"silu", MOE_ACT_SILU},
+      {"identity", MOE_ACT_IDENTITY}, {"swiglu", MOE_ACT_SWIGLU}};
+  for (const auto& kv : kNames)
+    if (std::strcmp(kv.first, name) == 0) {
+      *act = kv.second;
+      return MOE_OK;
+    }
+  return fail(MOE_INVALID_ARGUMENT, std::string("unsupported activation_type ") + name);
+}
+
+moe_status moe_kernel_create(const char* op_type, const moe_attributes* attrs, moe_kernel** out) {
+  try {
+    if (!op_type || !attrs || !out) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const bool q = std::strcmp(op_type, "QMoE") == 0;
+    if (!q && std::strcmp(op_type, "MoE") != 0)
+      return fail(MOE_INVALID_ARGUMENT, std::string("unknown op type ") + op_type);
+    const moe_attributes& a = *attrs;
+    if (a.activation_type < MOE_ACT_RELU || a.activation_type > MOE_ACT_SWIGLU)
+      return fail(MOE_INVALID_ARGUMENT, "invalid activation_type");
+    if (a.use_sparse_mixer) return fail(MOE_NOT_IMPLEMENTED, "use_sparse_mixer is not supported");
+    if (a.swiglu_fusion < 0 || a.swiglu_fusion > 2)
+      return fail(MOE_INVALID_ARGUMENT, "swiglu_fusion must be 0, 1 or 2");
+    if (a.k < 1) return fail(MOE_INVALID_ARGUMENT, "k must be >= 1");
+    if (q && a.expert_weight_bits != 4 && a.expert_weight_bits != 8)
+      return fail(MOE_INVALID_ARGUMENT, "expert_weight_bits must be 4 or 8, got " +
+                                            std::to_string(a.expert_weight_bits));
+    if (a.block_size < 0) return fail(MOE_INVALID_ARGUMENT, "block_size must be >= 0");
+    if (a.block_size > 0 && (a.block_size < 16 || (a.block_size & (a.block_size - 1))))
+      return fail(MOE_INVALID_ARGUMENT, "block_size must be a power of two >= 16");
+    auto* k = new moe_kernel();
+    k->quantized = q;
+    k->attrs = a;
+    *out = k;
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
+moe_status moe_kernel_set_expert_path(moe_kernel* kernel, int32_t path) {
+  if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+  if (path < -1 || path > moe::kPathPrefill) return fail(MOE_INVALID_ARGUMENT, "path must be -1..2");
+  kernel->forced_path = path;
+  return MOE_OK;
+}
+
+moe_status moe_kernel_workspace_size(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n,
+                                     size_t* bytes) {
+  try {
+    if (!kernel || !bytes) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    Problem p;
+    const moe_status st = validate(kernel, inputs, n, &p);
+    if (st != MOE_OK) return st;
+    *bytes = plan_layout(p).total;
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
+moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n,
+                                       moe_workspace_layout* out) {
+  try {
+    if (!kernel || !out) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    Problem p;
+    const moe_status st = validate(kernel, inputs, n, &p);
+    if (st != MOE_OK) return st;
+    const Layout l = plan_layout(p);
+    out->topk_ids = l.topk_ids;
+    out->topk_w = l.topk_w;
+    out->offsets = l.offsets;
+    out->perm = l.perm;
+    out->inv_perm = l.inv_perm;
+    out->total = l.total;
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
+moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
+                              void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  try {
+    if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+    Problem p;
+    moe_status st = validate(kernel, inputs, n, &p);
+    if (st != MOE_OK) return st;
+    if (p.T == 0) return MOE_OK;
+    if (!output) return fail(MOE_INVALID_ARGUMENT, "null output");
+    const Layout l = plan_layout(p);
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    if (ws) {
+      if (workspace_bytes < l.total)
+        return fail(MOE_INVALID_ARGUMENT, "workspace too small: need " + std::to_string(l.total) + " bytes");
+    } else {
+      int dev = 0;
+      hipError_t e = hipGetDevice(&dev);
+      if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+      auto* mk = const_cast<moe_kernel*>(kernel);
+      std::lock_guard<std::mutex> lock(mk->mu);
+      auto& slot = mk->ws_cache[{dev, stream_ptr}];
+      if (slot.second < l.total) {
+        if (slot.first) {
+          // the previous buffer may still be in use by work queued on this stream
+          e = hipStreamSynchronize(stream);
+          if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+          (void)hipFree(slot.first);
+          slot = {nullptr, 0};
+        }
+        void* buf = nullptr;
+        e = hipMalloc(&buf, l.total);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+        slot = {buf, l.total};
+      }
+      ws = static_cast<uint8_t*>(slot.first);
+    }
+
+    moe::RouteArgs ra{};
+    ra.p.logits = p.in[1]->data;
+    ra.p.logits_type = p.act_type;
+    ra.p.normalize = kernel->attrs.normalize_routing_weights;
+    ra.p.sigmoid = kernel->attrs.router_sigmoid;
+    ra.p.num_tokens = p.T;
+    ra.p.num_experts = p.E;
+    ra.p.k = p.k;
+    ra.p.topk_ids = reinterpret_cast<int32_t*>(ws + l.topk_ids);
+    ra.p.topk_w = reinterpret_cast<float*>(ws + l.topk_w);
+    ra.p.offsets = reinterpret_cast<int32_t*>(ws + l.offsets);
+    ra.p.perm = reinterpret_cast<int32_t*>(ws + l.perm);
+    ra.p.inv_perm = reinterpret_cast<int32_t*>(ws + l.inv_perm);
+    ra.p.scratch = ws + l.route_scratch;
+    ra.p.scratch_bytes = l.route_scratch_bytes;
+    ra.tile_offsets = reinterpret_cast<int32_t*>(ws + l.tile_offsets);
+    ra.tile_m = moe::kPrefillTileM;
+    hipError_t e = moe::launch_route_dispatch(ra, stream);
+    if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+
+    const moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
+    const int path = choose_path(kernel, a);
+    if (path < 0) return fail(MOE_NOT_IMPLEMENTED, "forced expert path does not support this problem");
+    switch (path) {
+      case moe::kPathDecode:
+        e = moe::launch_fc1_decode(a, stream);
+        if (e == hipSuccess) e = moe::launch_fc2_decode(a, stream);
+        break;
+      case moe::kPathPrefill:
+        e = moe::launch_fc1_prefill(a, stream);
+        if (e == hipSuccess) e = moe::launch_fc2_prefill(a, stream);
+        break;
+      default:
+        e = moe::launch_fc1_simt(a, stream);
+        if (e == hipSuccess) e = moe::launch_fc2_simt(a, stream);
+        break;
+    }
+    if (e != hipSuccess) return hip_fail(e, "expert launch");
+    e = moe::launch_finalize(a, stream);
+    if (e != hipSuccess) return hip_fail(e, "finalize launch");
+    return MOE_OK;
+  } catch (const std::bad_alloc&) {
+    return fail(MOE_FAIL, "out of host memory");
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
+void moe_kernel_release(moe_kernel* kernel) { delete kernel; }
+
+const char* moe_last_error(void) { return g_last_error.c_str(); }
+
+size_t moe_route_dispatch_scratch_size(int64_t num_tokens, int64_t num_experts, int64_t k) {
+  return moe::route_scratch_bytes(num_tokens, num_experts, k);
+}
+
+moe_status moe_route_dispatch_launch(const moe_route_params* params, void* stream) {
+  if (!params) return fail(MOE_INVALID_ARGUMENT, "null params");
+  const moe_route_params& p = *params;
+  if (p.num_tokens < 0 || p.num_experts <= 0 || p.k < 1 || p.k > p.num_experts)
+    return fail(MOE_INVALID_ARGUMENT, "bad routing shape");
+  if (p.num_experts > moe::kMaxExperts || p.k > moe::kMaxTopK)
+    return fail(MOE_NOT_IMPLEMENTED, "routing shape beyond supported limits");
+  if (!is_float_type(p.logits_type)) return fail(MOE_INVALID_ARGUMENT, "bad logits type");
+  if (p.num_tokens > 0 && (!p.logits || !p.topk_ids || !p.topk_w || !p.offsets || !p.perm || !p.inv_perm))
+    return fail(MOE_INVALID_ARGUMENT, "null routing buffer");
+  const size_t need = moe::route_scratch_bytes(p.num_tokens, p.num_experts, p.k);
+  if (need > 0 && (!p.scratch || p.scratch_bytes < need))
+    return fail(MOE_INVALID_ARGUMENT, "routing scratch too small: need " + std::to_string(need));
+  moe::RouteArgs ra{};
+  ra.p = p;
+  ra.tile_offsets = nullptr;
+  ra.tile_m = moe::kPrefillTileM;
+  const hipError_t e = moe::launch_route_dispatch(ra, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+  return MOE_OK;
+}
+
+const char* moe_version(void) { return "moe-mi355x 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+"""Host-side mirror of the com.microsoft MoE / QMoE op kernels.
+
+One object per graph node, like the reference's kernel object: attributes are
+fixed at construction (musa/ep/src/kernels/llm/attention.cc:63-72 reads them
+in the constructor through AttrOrDefault, kernel_attributes.h:21-28), and each
+call validates inputs and enqueues the HIP kernels on the current torch stream
+(the role of Compute, attention.cc:100-256).  Inputs follow the op schema
+order; pass None for an absent optional input.  Tensors must be contiguous
+and resident on the GPU: torch provides device memory and streams only, all
+arithmetic runs in lib/libmoe_mi355x.so.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+
+from ._capi import (ACTIVATIONS, ELEM_BFLOAT16, ELEM_FLOAT, ELEM_FLOAT16, ELEM_UINT8, PATHS,
+                    MoeAttributes, MoeError, MoeRouteParams, MoeTensor, MoeWorkspaceLayout, check,
+                    load_library)
+
+_ELEM = {torch.float32: ELEM_FLOAT, torch.float16: ELEM_FLOAT16, torch.bfloat16: ELEM_BFLOAT16,
+         torch.uint8: ELEM_UINT8}
+
+MOE_INPUTS = ("input", "router_probs", "fc1_experts_weights", "fc1_experts_bias", "fc2_experts_weights",
+              "fc2_experts_bias", "fc3_experts_weights", "fc3_experts_bias")
+QMOE_INPUTS = ("input", "router_probs", "fc1_experts_weights", "fc1_scales", "fc1_experts_bias",
+               "fc2_experts_weights", "fc2_scales", "fc2_experts_bias", "fc3_experts_weights", "fc3_scales",
+               "fc3_experts_bias")
+
+
+def _tensor_desc(t: Optional[torch.Tensor]) -> MoeTensor:
+    d = MoeTensor()
+    if t is None:
+        d.data = None
+        return d
+    if not t.is_cuda:
+        raise ValueError("MoE inputs must be GPU tensors")
+    if not t.is_contiguous():
+        raise ValueError("MoE inputs must be contiguous")
+    if t.dim() > 4:
+        raise ValueError("rank > 4")
+    if t.dtype not in _ELEM:
+        raise ValueError(f"unsupported dtype {t.dtype}")
+    d.data = t.data_ptr() if t.numel() else 1  # non-null marker for empty tensors
+    d.elem_type = _ELEM[t.dtype]
+    d.rank = t.dim()
+    for i, s in enumerate(t.shape):
+        d.dims[i] = s
+    return d
+
+
+class _MoEOp:
+    op_type = "MoE"
+    input_names: Sequence[str] = MOE_INPUTS
+
+    def __init__(self, *, k: int = 1, activation_type: str = "relu", normalize_routing_weights: int = 0,
+                 use_sparse_mixer: int = 0, swiglu_fusion: int = 0, swiglu_limit: Optional[float] = None,
+                 activation_alpha: float = 1.0, activation_beta: float = 0.0, expert_weight_bits: int = 4,
+                 block_size: int = 0, router_sigmoid: int = 0, expert_path: str = "auto"):
+        self._lib = load_library()
+        lib = self._lib
+        a = MoeAttributes()
+        check(lib.moe_attributes_init(ctypes.byref(a), self.op_type.encode()))
+        act = ctypes.c_int32()
+        check(lib.moe_parse_activation(activation_type.encode(), ctypes.byref(act)))
+        a.k = int(k)
+        a.activation_type = act.value
+        a.normalize_routing_weights = int(normalize_routing_weights)
+        a.use_sparse_mixer = int(use_sparse_mixer)
+        a.swiglu_fusion = int(swiglu_fusion)
+        if swiglu_limit is not None:
+            a.has_swiglu_limit = 1
+            a.swiglu_limit = float(swiglu_limit)
+        a.activation_alpha = float(activation_alpha)
+        a.activation_beta = float(activation_beta)
+        if self.op_type == "QMoE":
+            a.expert_weight_bits = int(expert_weight_bits)
+            a.block_size = int(block_size or 0)
+        a.router_sigmoid = int(router_sigmoid)
+        h = ctypes.c_void_p()
+        check(lib.moe_kernel_create(self.op_type.encode(), ctypes.byref(a), ctypes.byref(h)))
+        self._h = h
+        self.attributes = a
+        if expert_path != "auto":
+            check(lib.moe_kernel_set_expert_path(h, PATHS[expert_path]))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.moe_kernel_release(h)
+            self._h = None
+
+    def _descs(self, inputs):
+        if len(inputs) > len(self.input_names):
+            raise ValueError(f"{self.op_type} takes at most {len(self.input_names)} inputs")
+        arr = (MoeTensor * len(inputs))(*[_tensor_desc(t) for t in inputs])
+        return arr, len(inputs)
+
+    def workspace_size(self, *inputs) -> int:
+        arr, n = self._descs(inputs)
+        out = ctypes.c_size_t()
+        check(self._lib.moe_kernel_workspace_size(self._h, arr, n, ctypes.byref(out)))
+        return out.value
+
+    def workspace_layout(self, *inputs) -> dict:
+        arr, n = self._descs(inputs)
+        lay = MoeWorkspaceLayout()
+        check(self._lib.moe_kernel_workspace_layout(self._h, arr, n, ctypes.byref(lay)))
+        return {name: getattr(lay, name) for name, _ in MoeWorkspaceLayout._fields_}
+
+    def __call__(self, *inputs, out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                 stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        arr, n = self._descs(inputs)
+        x = inputs[0]
+        if out is None:
+            out = torch.empty_like(x)
+        elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("out must match the input's shape and dtype")
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        check(self._lib.moe_kernel_compute(self._h, arr, n, out.data_ptr() if out.numel() else None, ws_ptr,
+                                           ws_bytes, ctypes.c_void_p(s.cuda_stream)))
+        return out
+
+
+class MoE(_MoEOp):
+    """com.microsoft MoE (float expert weights)."""
+    op_type = "MoE"
+    input_names = MOE_INPUTS
+
+
+class QMoE(_MoEOp):
+    """com.microsoft QMoE (int8 / int4 expert weights with scales)."""
+    op_type = "QMoE"
+    input_names = QMOE_INPUTS
+
+
+def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoid: bool = False,
+                   stream: Optional[torch.cuda.Stream] = None) -> dict:
+    """Runs the router + dispatch stage alone.  Returns device tensors
+    topk_ids [T, k], topk_w [T, k], offsets [E+1], perm [T*k], inv_perm [T*k]."""
+    lib = load_library()
+    if logits.dim() != 2:
+        raise ValueError("logits must be [T, E]")
+    T, E = logits.shape
+    dev = logits.device
+    res = {
+        "topk_ids": torch.empty((T, k), dtype=torch.int32, device=dev),
+        "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
+        "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
+        "perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
+        "inv_perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
+    }
+    nscratch = lib.moe_route_dispatch_scratch_size(T, E, k)
+    scratch = torch.empty((max(nscratch, 1),), dtype=torch.uint8, device=dev)
+    p = MoeRouteParams()
+    p.logits = logits.data_ptr() if logits.numel() else None
+    p.logits_type = _ELEM[logits.dtype]
+    p.normalize = int(normalize)
+    p.sigmoid = int(sigmoid)
+    p.num_tokens, p.num_experts, p.k = T, E, k
+    for name in ("topk_ids", "topk_w", "offsets", "perm", "inv_perm"):
+        setattr(p, name, res[name].data_ptr() if res[name].numel() else None)
+    p.scratch = scratch.data_ptr()
+    p.scratch_bytes = nscratch
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
+    check(lib.moe_route_dispatch_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
+    return res
+
+
+__all__ = ["MoE", "QMoE", "route_dispatch", "MoeError", "MOE_INPUTS", "QMOE_INPUTS"]

@@ -1,0 +1,208 @@
+"""ctypes wrapper of the C restatement (oracle/libmoe_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, and only as the checker.  The product library
+never loads it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "libmoe_oracle.so"
+
+ORC_F32, ORC_U8, ORC_F16, ORC_BF16 = 1, 2, 10, 16
+ACT = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
+_DT = {"f32": ORC_F32, "f16": ORC_F16, "bf16": ORC_BF16}
+
+
+class OrcArgs(ctypes.Structure):
+    _fields_ = [
+        ("num_tokens", ctypes.c_int64), ("hidden", ctypes.c_int64), ("inter", ctypes.c_int64),
+        ("num_experts", ctypes.c_int64), ("k", ctypes.c_int64),
+        ("activation", ctypes.c_int32), ("normalize", ctypes.c_int32), ("swiglu_fusion", ctypes.c_int32),
+        ("swiglu_limit", ctypes.c_float), ("alpha", ctypes.c_float), ("beta", ctypes.c_float),
+        ("router_sigmoid", ctypes.c_int32), ("quant_bits", ctypes.c_int32), ("block_size", ctypes.c_int64),
+        ("act_dtype", ctypes.c_int32), ("scale_dtype", ctypes.c_int32),
+        ("x", ctypes.c_void_p), ("logits", ctypes.c_void_p),
+        ("w1", ctypes.c_void_p), ("s1", ctypes.c_void_p), ("b1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p), ("s2", ctypes.c_void_p), ("b2", ctypes.c_void_p),
+        ("w3", ctypes.c_void_p), ("s3", ctypes.c_void_p), ("b3", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("topk_ids", ctypes.c_void_p), ("topk_w", ctypes.c_void_p), ("expert_offsets", ctypes.c_void_p),
+        ("perm", ctypes.c_void_p), ("out_f32", ctypes.c_void_p), ("token_mask", ctypes.c_void_p),
+        ("num_threads", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            raise FileNotFoundError(f"{LIB} missing: run make -C oracle")
+        lib = ctypes.CDLL(str(LIB))
+        lib.orc_moe_forward.argtypes = [ctypes.POINTER(OrcArgs)]
+        lib.orc_moe_forward.restype = ctypes.c_int
+        lib.orc_route.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                  ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+        lib.orc_route.restype = ctypes.c_int
+        lib.orc_dispatch.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.c_void_p, ctypes.c_void_p]
+        lib.orc_dispatch.restype = ctypes.c_int
+        lib.orc_dequant.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+        lib.orc_dequant.restype = ctypes.c_int
+        lib.orc_activation.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                       ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                       ctypes.c_void_p]
+        lib.orc_activation.restype = None
+        for n in ("orc_f16_to_f32", "orc_bf16_to_f32"):
+            getattr(lib, n).argtypes = [ctypes.c_uint16]
+            getattr(lib, n).restype = ctypes.c_float
+        for n in ("orc_f32_to_f16", "orc_f32_to_bf16"):
+            getattr(lib, n).argtypes = [ctypes.c_float]
+            getattr(lib, n).restype = ctypes.c_uint16
+        _lib = lib
+    return _lib
+
+
+def _ptr(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def route(logits: np.ndarray, k: int, normalize: bool = False, sigmoid: bool = False):
+    """fp32 logits [T, E] -> (ids [T,k] int32, w [T,k] float32)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = lg.shape
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    rc = load().orc_route(_ptr(lg), T, E, k, int(normalize), int(sigmoid), _ptr(ids), _ptr(w))
+    if rc:
+        raise ValueError(f"orc_route rc={rc}")
+    return ids, w
+
+
+def dispatch(ids: np.ndarray, E: int):
+    """ids [T, k] -> (offsets [E+1], perm [T*k])."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    T, k = ids.shape
+    offs = np.zeros(E + 1, np.int32)
+    perm = np.zeros(T * k, np.int32)
+    rc = load().orc_dispatch(_ptr(ids), T, k, E, _ptr(offs), _ptr(perm))
+    if rc:
+        raise ValueError(f"orc_dispatch rc={rc}")
+    return offs, perm
+
+
+def dequant(q: np.ndarray, scales: np.ndarray, scale_dtype: str, bits: int, block: int, N: int, K: int):
+    out = np.zeros((N, K), np.float32)
+    rc = load().orc_dequant(_ptr(np.ascontiguousarray(q)), _ptr(np.ascontiguousarray(scales)), _DT[scale_dtype],
+                            bits, block, N, K, _ptr(out))
+    if rc:
+        raise ValueError(f"orc_dequant rc={rc}")
+    return out
+
+
+def activation(h1: np.ndarray, h3: Optional[np.ndarray], inter: int, act: str, fusion: int = 0,
+               alpha: float = 1.0, beta: float = 0.0, limit: float = float("inf")) -> np.ndarray:
+    h1 = np.ascontiguousarray(h1, dtype=np.float32)
+    h3 = None if h3 is None else np.ascontiguousarray(h3, dtype=np.float32)
+    out = np.zeros(inter, np.float32)
+    load().orc_activation(_ptr(h1), _ptr(h3), inter, ACT[act], fusion, alpha, beta, limit, _ptr(out))
+    return out
+
+
+def moe_forward(*, x, logits, w1, w2, k, hidden, inter, experts, act_dtype="f32", activation="relu",
+                normalize=0, swiglu_fusion=0, swiglu_limit=None, alpha=1.0, beta=0.0, router_sigmoid=0,
+                bits=0, block_size=0, scale_dtype="f16", s1=None, b1=None, s2=None, b2=None, w3=None,
+                s3=None, b3=None, token_mask=None, threads=0):
+    """Runs the restated op.  Arrays are numpy in their storage types (bf16 as
+    uint16).  Returns dict(out, out_f32, topk_ids, topk_w, offsets, perm)."""
+    T = x.shape[0]
+    a = OrcArgs()
+    a.num_tokens, a.hidden, a.inter, a.num_experts, a.k = T, hidden, inter, experts, k
+    a.activation = ACT[activation]
+    a.normalize = int(normalize)
+    a.swiglu_fusion = int(swiglu_fusion)
+    a.swiglu_limit = float("inf") if swiglu_limit is None else float(swiglu_limit)
+    a.alpha, a.beta = alpha, beta
+    a.router_sigmoid = int(router_sigmoid)
+    a.quant_bits = int(bits)
+    a.block_size = int(block_size or 0)
+    a.act_dtype = _DT[act_dtype]
+    a.scale_dtype = _DT[scale_dtype]
+    keep = []
+
+    def c(arr):
+        if arr is None:
+            return None
+        arr = np.ascontiguousarray(arr)
+        keep.append(arr)
+        return arr.ctypes.data
+
+    a.x, a.logits = c(x), c(logits)
+    a.w1, a.s1, a.b1 = c(w1), c(s1), c(b1)
+    a.w2, a.s2, a.b2 = c(w2), c(s2), c(b2)
+    a.w3, a.s3, a.b3 = c(w3), c(s3), c(b3)
+    out = np.zeros(x.shape, dtype=x.dtype)
+    out_f32 = np.zeros((T, hidden), np.float32)
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    offs = np.zeros(experts + 1, np.int32)
+    perm = np.zeros(T * k, np.int32)
+    a.out, a.out_f32 = out.ctypes.data, out_f32.ctypes.data
+    a.topk_ids, a.topk_w, a.expert_offsets, a.perm = ids.ctypes.data, w.ctypes.data, offs.ctypes.data, perm.ctypes.data
+    if token_mask is not None:
+        a.token_mask = c(np.asarray(token_mask, dtype=np.uint8))
+    a.num_threads = int(threads)
+    rc = load().orc_moe_forward(ctypes.byref(a))
+    if rc:
+        raise ValueError(f"orc_moe_forward rc={rc}")
+    return dict(out=out, out_f32=out_f32, topk_ids=ids, topk_w=w, offsets=offs, perm=perm)
+
+
+def forward_problem(cfg, host: dict, token_mask=None, threads=0):
+    """Runs the oracle on a workloads.Problem's inputs copied to the host
+    (dict name -> numpy array, names as in the op schema)."""
+    return moe_forward(
+        x=host["input"], logits=host["router_probs"], w1=host["fc1_experts_weights"],
+        w2=host["fc2_experts_weights"], k=cfg.k, hidden=cfg.hidden, inter=cfg.inter, experts=cfg.experts,
+        act_dtype=cfg.dtype, activation=cfg.activation, normalize=cfg.normalize, swiglu_fusion=cfg.swiglu_fusion,
+        swiglu_limit=cfg.swiglu_limit, alpha=cfg.alpha, beta=cfg.beta, bits=cfg.bits, block_size=cfg.block_size,
+        scale_dtype=cfg.scale_dtype, s1=host.get("fc1_scales"), b1=host.get("fc1_experts_bias"),
+        s2=host.get("fc2_scales"), b2=host.get("fc2_experts_bias"), w3=host.get("fc3_experts_weights"),
+        s3=host.get("fc3_scales"), b3=host.get("fc3_experts_bias"), token_mask=token_mask, threads=threads)
+
+
+def f16_bits_to_f32(u16: np.ndarray) -> np.ndarray:
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+def bf16_bits_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """RNE, as the reference's float32_to_bfloat16_bits (test/ops/op_test_utils.py:235-245)."""
+    bits = np.asarray(x, np.float32).view(np.uint32)
+    return ((bits + np.uint32(0x7FFF) + ((bits >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+def to_f32(arr: np.ndarray, dtype: str) -> np.ndarray:
+    if dtype == "bf16":
+        return bf16_bits_to_f32(arr)
+    return np.asarray(arr).astype(np.float32)
+
+
+os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
