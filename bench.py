@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""MoE / QMoE layer benchmark on one MI355X.
+
+A step is one QMoE layer invocation (router + dispatch + fc1/fc3 + activation
++ fc2 + finalize) over one batch of synthetic tokens whose inputs and weights
+are already resident in HBM.  The headline workload is BASELINE.json's
+QMoE int8 per-output-channel (fp16 scales), Mixtral shape
+(H=4096, I=14336, E=8, top-2, SwiGLU fc1/fc3 unfused), fp16 activations, at
+16 tokens (decode).  The other configurations are reported under "extra".
+
+Roofline: the dominant kernel's algorithmic bytes (decode) or FLOPs (prefill)
+per launch divided by its mean duration, timed with HIP events recorded by the
+library on the stream the kernels run on (moe_kernel_stage_times).
+
+cpu_baseline: the oracle (C restatement, OpenMP) on the same inputs on the
+host cores of this box.  It is a reported baseline, not the target.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "onnxruntime-musa_amd" / "python"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0   # MI355X HBM3E
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+
+METRIC = "QMoE layer tokens/s; HBM GB/s at decode, MFMA TFLOP/s at prefill, % roofline"
+HEADLINE = ("c2_qmoe_int8_mixtral", 16)
+EXTRA = [("c2_qmoe_int8_mixtral", 1), ("c2_qmoe_int8_mixtral", 4096),
+         ("c3_qmoe_int4_mixtral", 1), ("c3_qmoe_int4_mixtral", 16), ("c3_qmoe_int4_mixtral", 4096),
+         ("c4_qmoe_int4_gptoss", 1), ("c4_qmoe_int4_gptoss", 64), ("c4_qmoe_int4_gptoss", 8192),
+         ("c5_moe_f16_qwen3", 8192), ("c1_moe_f32", 64)]
+
+
+def esz(dt: str) -> int:
+    return 4 if dt == "f32" else 2
+
+
+def expert_bytes(cfg, part: str) -> int:
+    """HBM bytes of one expert's weights + scales + biases for fc1 (incl. fc3) or fc2."""
+    H, I = cfg.hidden, cfg.inter
+    mats = [(cfg.n1, H)] + ([(I, H)] if cfg.use_fc3 else []) if part == "fc1" else [(H, I)]
+    total = 0
+    for n, k in mats:
+        if cfg.bits:
+            total += n * k * cfg.bits // 8
+            total += n * (k // cfg.block_size if cfg.block_size else 1) * esz(cfg.scale_dtype)
+        else:
+            total += n * k * esz(cfg.dtype)
+        if cfg.bias:
+            total += n * esz(cfg.dtype)
+    return total
+
+
+def kernel_cost(cfg, T: int, hit: int):
+    """Algorithmic bytes and FLOPs per launch of the fc1 and fc2 kernels."""
+    rows = T * cfg.k
+    a = esz(cfg.dtype)
+    fc1_bytes = hit * expert_bytes(cfg, "fc1") + T * cfg.hidden * a + rows * cfg.inter * a
+    fc2_bytes = hit * expert_bytes(cfg, "fc2") + rows * cfg.inter * a + rows * cfg.hidden * 4
+    n1_total = cfg.n1 + (cfg.inter if cfg.use_fc3 else 0)
+    fc1_flops = rows * 2 * n1_total * cfg.hidden
+    fc2_flops = rows * 2 * cfg.hidden * cfg.inter
+    layer_bytes = (hit * (expert_bytes(cfg, "fc1") + expert_bytes(cfg, "fc2")) + T * cfg.hidden * a * 2
+                   + T * cfg.experts * a)
+    return dict(fc1_bytes=fc1_bytes, fc2_bytes=fc2_bytes, fc1_flops=fc1_flops, fc2_flops=fc2_flops,
+                layer_bytes=layer_bytes, layer_flops=fc1_flops + fc2_flops)
+
+
+def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=False):
+    import torch
+
+    from onnxruntime_musa_amd.workloads import CONFIGS, make_problem
+
+    cfg = CONFIGS[name]
+    prob = make_problem(cfg, T, seed=1234, device=dev)
+    op = prob.make_op()
+    inputs = prob.schema_inputs()
+    ws = torch.empty((op.workspace_size(*inputs),), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(inputs[0])
+    call = op.bind(*inputs, out=out, workspace=ws)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        call()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = max(start.elapsed_time(stop), wall * 1e3) / steps
+    # routing of this workload: experts actually hit
+    lay = op.workspace_layout(*inputs)
+    offs = ws[lay["offsets"]:lay["offsets"] + 4 * (cfg.experts + 1)].view(torch.int32).cpu()
+    hit = int((offs[1:] - offs[:-1] > 0).sum())
+    # per-stage timing pass (events recorded by the library on the kernels' stream)
+    op.set_profiling(True)
+    stages = []
+    for _ in range(steps):
+        call()
+        stages.append(op.stage_times())
+    op.set_profiling(False)
+    path = stages[-1]["path"]
+    st = {k: statistics.mean(s[k] for s in stages) for k in ("route_dispatch", "fc1", "fc2", "finalize")}
+    cost = kernel_cost(cfg, T, hit)
+    decode = path != "prefill"
+    if decode:
+        fc1_ach = cost["fc1_bytes"] / (st["fc1"] * 1e-3) / 1e9
+        roof = dict(bound="hbm", achieved=round(fc1_ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                    frac=round(fc1_ach / PEAK_HBM_GBS, 4), traffic=None)
+    else:
+        fc1_ach = cost["fc1_flops"] / (st["fc1"] * 1e-3) / 1e12
+        roof = dict(bound="mfma", achieved=round(fc1_ach, 1), peak=PEAK_MFMA_TFLOPS, unit="TFLOP/s",
+                    frac=round(fc1_ach / PEAK_MFMA_TFLOPS, 4), traffic=None)
+    layer_s = ms_per_step * 1e-3
+    res = dict(workload=name, tokens=T, path=path, ms_per_step=round(ms_per_step, 4),
+               tokens_per_s=round(T / layer_s, 1), experts_hit=hit,
+               layer_hbm_gbs=round(cost["layer_bytes"] / layer_s / 1e9, 1),
+               layer_tflops=round(cost["layer_flops"] / layer_s / 1e12, 2),
+               stages_ms={k: round(v, 4) for k, v in st.items()},
+               fc2=dict(achieved_gbs=round(cost["fc2_bytes"] / (st["fc2"] * 1e-3) / 1e9, 1),
+                        achieved_tflops=round(cost["fc2_flops"] / (st["fc2"] * 1e-3) / 1e12, 2)),
+               roofline=roof, algorithmic=dict(fc1_bytes=cost["fc1_bytes"], fc1_flops=cost["fc1_flops"]))
+    if keep_problem:
+        return res, prob
+    del op, ws, out, call, prob, inputs
+    torch.cuda.empty_cache()
+    return res, None
+
+
+def cpu_baseline(prob, budget_s: float = 12.0):
+    """Times the oracle on the headline workload on this host's cores."""
+    import numpy as np
+
+    from onnxruntime_musa_amd.workloads import to_host
+    from oracle import oracle
+
+    cores = int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
+    cores = max(1, min(cores, 16, len(os.sched_getaffinity(0))))
+    host = {n: to_host(t) for n, t in prob.inputs.items()}
+    oracle.forward_problem(prob.cfg, host, threads=cores)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        oracle.forward_problem(prob.cfg, host, threads=cores)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return dict(value=round(prob.tokens / med, 2), unit="tokens/s", cores=cores, kind="port",
+                sample=f"{prob.cfg.name} full layer, {prob.tokens} tokens, {len(times)} timed runs "
+                       f"(median {med * 1e3:.1f} ms), OpenMP fp32 restatement")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", default=None, help="name:tokens to run instead of the headline")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (PMC byte-counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the MoE layer runs on a single MI355X; multi-GPU sharding is design-only).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones((n,), dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": args.steps}), flush=True)
+        return
+    name, T = HEADLINE
+    if args.workload:
+        name, t = args.workload.split(":")
+        T = int(t)
+    head, prob = run_workload(name, T, args.steps, args.warmup, dev, keep_problem=True)
+    print(f"[bench] {name} T={T}: {head['tokens_per_s']} tok/s, {head['ms_per_step']} ms, "
+          f"fc1 {head['roofline']['achieved']} {head['roofline']['unit']}", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(prob)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    del prob
+    torch.cuda.empty_cache()
+    extra = []
+    if not args.no_extra and not args.workload:
+        for wname, wT in EXTRA:
+            r, _ = run_workload(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev)
+            extra.append(r)
+            print(f"[bench] {wname} T={wT}: {r['tokens_per_s']} tok/s, {r['ms_per_step']} ms, path={r['path']}, "
+                  f"fc1 {r['roofline']['achieved']} {r['roofline']['unit']} ({r['roofline']['frac']:.1%})",
+                  file=sys.stderr, flush=True)
+    from onnxruntime_musa_amd.workloads import CONFIGS
+    cfg = CONFIGS[name]
+    line = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype,
+        "data": "synthetic",
+        "config": {"workload": name, "tokens": T, "hidden": cfg.hidden, "inter": cfg.inter,
+                   "experts": cfg.experts, "k": cfg.k,
+                   "weights": (f"int{cfg.bits} " + (f"block {cfg.block_size}" if cfg.block_size else "per-channel")
+                               + f", {cfg.scale_dtype} scales") if cfg.bits else cfg.dtype,
+                   "path": head["path"], "experts_hit": head["experts_hit"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "stages_ms": head["stages_ms"],
+        "layer_hbm_gbs": head["layer_hbm_gbs"],
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -150,6 +150,16 @@ MOE_API moe_status moe_kernel_workspace_layout(const moe_kernel *kernel, const m
  * Call before the kernel is shared between threads. */
 MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
 
+/* Stage profiling (the role of the reference's EP profiler hooks,
+ * musa/ep/src/ep_profiling.cc:141-288, with real producers): when enabled,
+ * moe_kernel_compute records HIP events on its stream around each stage.
+ * moe_kernel_stage_times waits for the last call's events and returns the
+ * stage durations in milliseconds: ms[0] router+dispatch, ms[1] fc1 (+fc3,
+ * activation), ms[2] fc2, ms[3] finalize; *path receives the expert-kernel
+ * family used (0 SIMT, 1 decode, 2 prefill).  Single-threaded use only. */
+MOE_API moe_status moe_kernel_set_profiling(moe_kernel *kernel, int32_t enable);
+MOE_API moe_status moe_kernel_stage_times(moe_kernel *kernel, float *ms, int32_t *path);
+
 /* Message of the last non-OK status returned on this thread. */
 MOE_API const char *moe_last_error(void);
 

@@ -1,0 +1,17 @@
+// moe_expert_decode_int4.hip -- int4 instantiations of the decode expert kernels
+// (kernel templates: moe_expert_decode.h, moe_expert_decode_lds.h).
+#include "moe_expert_decode_lds.h"
+
+namespace moe {
+namespace decode {
+
+hipError_t launch_int4(const Stage& st, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+  return launch_quant<kInt4>(st, a, fc1, gated, stream);
+}
+
+hipError_t launch_lds_int4(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+  return launch_lds_fmt<kInt4>(ls, a, fc1, gated, stream);
+}
+
+}  // namespace decode
+}  // namespace moe

@@ -99,7 +99,8 @@ __global__ void __launch_bounds__(256) fc2_simt_kernel(ExpertArgs a) {
   }
 }
 
-// out[t, h] = sum_j w[t, j] * y2[inv_perm[t*k + j], h], summed in slot order.
+// out[t, h] = sum_j w[t, j] * y2[inv_perm[t*k + j], h], summed in slot order
+// (y2 itself the fixed-order sum of its partial planes when fc2 split K).
 template <typename OT>
 __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   const int64_t t = blockIdx.x;
@@ -109,15 +110,27 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   for (int64_t j = 0; j < a.k; ++j) {
     const int64_t f = t * a.k + j;
     const float w = a.topk_w[f];
+    const int64_t plane = a.T * a.k * a.H;
     const float* y = a.y2 + static_cast<int64_t>(a.inv_perm[f]) * a.H;
     if (h0 + 4 <= a.H && (a.H % 4) == 0) {
-      const float4 v = *reinterpret_cast<const float4*>(y + h0);
+      float4 v = *reinterpret_cast<const float4*>(y + h0);
+      for (int z = 1; z < a.y2_planes; ++z) {  // partial sums over K, fixed order
+        const float4 u = *reinterpret_cast<const float4*>(y + z * plane + h0);
+        v.x += u.x;
+        v.y += u.y;
+        v.z += u.z;
+        v.w += u.w;
+      }
       acc[0] += w * v.x;
       acc[1] += w * v.y;
       acc[2] += w * v.z;
       acc[3] += w * v.w;
     } else {
-      for (int c = 0; c < 4 && h0 + c < a.H; ++c) acc[c] += w * y[h0 + c];
+      for (int c = 0; c < 4 && h0 + c < a.H; ++c) {
+        float v = y[h0 + c];
+        for (int z = 1; z < a.y2_planes; ++z) v += y[z * plane + h0 + c];
+        acc[c] += w * v;
+      }
     }
   }
   typename OT::storage* out = static_cast<typename OT::storage*>(a.out);

@@ -34,6 +34,8 @@ struct RouteArgs {
   moe_route_params p;
   int32_t* tile_offsets;  // optional [E+1]: prefix of ceil(count_e / tile_m)
   int32_t tile_m;
+  int32_t* zero;          // optional: counters cleared to 0 by the routing kernel
+  int64_t zero_count;
 };
 
 size_t route_scratch_bytes(int64_t T, int64_t E, int64_t k);
@@ -63,14 +65,17 @@ struct ExpertArgs {
   const void *w2, *s2, *b2;
   // intermediates
   void* act;   // [T*k, I] in act_type
-  float* y2;   // [T*k, H] fp32
+  float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
+  int32_t y2_planes;
+  float* fc1_part;        // decode fc1 partial planes (K split across workgroups)
+  int32_t* fc1_arrive;    // decode fc1 per-tile arrival counters (zeroed by routing)
   void* out;   // [T, H] act_type
 };
 
 hipError_t launch_fc1_simt(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream);
-hipError_t launch_fc2_decode(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
 hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_prefill(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
@@ -84,5 +89,21 @@ bool prefill_supported(const ExpertArgs& a);
 constexpr int kPrefillTileM = 128;
 // Largest token count served by the decode (weight-streaming) path.
 constexpr int64_t kDecodeMaxTokens = 64;
+// Token count up to which decode stages the activation rows in LDS.
+constexpr int64_t kLdsMaxTokens = 16;
+// Most K splits across workgroups of the decode fc2 kernel (partial planes of y2).
+constexpr int kMaxDecodeKsplit = 8;
+
+// Launch plan of the decode kernels, shared by the workspace planner and the
+// launchers so both agree on the partial-plane sizes.
+struct DecodePlan {
+  bool lds = false;         // activation slice staged in LDS (T <= kLdsMaxTokens)
+  int32_t ksg1 = 1, kr1 = 0, fgroups1 = 0;  // fc1 K groups, K per group, feature groups
+  int32_t ksg2 = 1, kr2 = 0;                // fc2 K groups, K per group
+  int64_t fc1_part_floats = 0;              // partial-plane storage of fc1
+  int64_t arrive_count = 0;                 // arrival counters of fc1
+  int32_t y2_planes_max = 1;
+};
+DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode);
 
 }  // namespace moe

@@ -66,8 +66,9 @@ struct Problem {
 
 // Workspace sections, byte offsets from the workspace base.
 struct Layout {
-  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, total;
+  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, fc1_part, arrive, total;
   size_t route_scratch_bytes;
+  moe::DecodePlan decode;
 };
 
 Layout plan_layout(const Problem& p) {
@@ -88,7 +89,11 @@ Layout plan_layout(const Problem& p) {
   l.route_scratch_bytes = moe::route_scratch_bytes(p.T, p.E, p.k);
   l.route_scratch = take(l.route_scratch_bytes);
   l.act = take(rows * static_cast<size_t>(p.I) * elem_size(p.act_type));
-  l.y2 = take(rows * static_cast<size_t>(p.H) * 4);
+  l.decode = moe::plan_decode(p.T, p.H, p.I, p.E, p.k, p.wfmt, p.gate_mode);
+  const size_t planes = static_cast<size_t>(std::max<int32_t>(1, l.decode.y2_planes_max));
+  l.y2 = take(rows * static_cast<size_t>(p.H) * 4 * planes);
+  l.fc1_part = take(static_cast<size_t>(l.decode.fc1_part_floats) * 4);
+  l.arrive = take(static_cast<size_t>(l.decode.arrive_count) * 4);
   l.total = o;
   return l;
 }
@@ -101,10 +106,17 @@ struct moe_kernel {
   int32_t forced_path = -1;
   std::mutex mu;
   std::map<std::pair<int, void*>, std::pair<void*, size_t>> ws_cache;  // (device, stream) -> buffer
+  // stage profiling
+  bool profiling = false;
+  hipEvent_t ev[5] = {};
+  bool ev_recorded = false;
+  int32_t last_path = -1;
 
   ~moe_kernel() {
     for (auto& kv : ws_cache)
       if (kv.second.first) (void)hipFree(kv.second.first);
+    for (auto& e : ev)
+      if (e) (void)hipEventDestroy(e);
   }
 };
 
@@ -279,6 +291,9 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   }
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
+  a.y2_planes = 1;
+  a.fc1_part = reinterpret_cast<float*>(ws + l.fc1_part);
+  a.fc1_arrive = reinterpret_cast<int32_t*>(ws + l.arrive);
   a.out = output;
   return a;
 }
@@ -462,29 +477,47 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     ra.p.scratch_bytes = l.route_scratch_bytes;
     ra.tile_offsets = reinterpret_cast<int32_t*>(ws + l.tile_offsets);
     ra.tile_m = moe::kPrefillTileM;
-    hipError_t e = moe::launch_route_dispatch(ra, stream);
-    if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
-
-    const moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
+    ra.zero = reinterpret_cast<int32_t*>(ws + l.arrive);
+    ra.zero_count = l.decode.arrive_count;
+    moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
     const int path = choose_path(kernel, a);
     if (path < 0) return fail(MOE_NOT_IMPLEMENTED, "forced expert path does not support this problem");
+
+    auto* mk = const_cast<moe_kernel*>(kernel);
+    const bool prof = mk->profiling;
+    hipError_t e = hipSuccess;
+    auto mark = [&](int i) {
+      if (prof && e == hipSuccess) e = hipEventRecord(mk->ev[i], stream);
+    };
+    mark(0);
+    e = e == hipSuccess ? moe::launch_route_dispatch(ra, stream) : e;
+    if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+    mark(1);
     switch (path) {
       case moe::kPathDecode:
         e = moe::launch_fc1_decode(a, stream);
-        if (e == hipSuccess) e = moe::launch_fc2_decode(a, stream);
+        mark(2);
+        if (e == hipSuccess) e = moe::launch_fc2_decode(a, &a.y2_planes, stream);
         break;
       case moe::kPathPrefill:
         e = moe::launch_fc1_prefill(a, stream);
+        mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_prefill(a, stream);
         break;
       default:
         e = moe::launch_fc1_simt(a, stream);
+        mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_simt(a, stream);
         break;
     }
     if (e != hipSuccess) return hip_fail(e, "expert launch");
+    mark(3);
     e = moe::launch_finalize(a, stream);
     if (e != hipSuccess) return hip_fail(e, "finalize launch");
+    mark(4);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    mk->last_path = path;
+    mk->ev_recorded = prof;
     return MOE_OK;
   } catch (const std::bad_alloc&) {
     return fail(MOE_FAIL, "out of host memory");
@@ -494,6 +527,32 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
 }
 
 void moe_kernel_release(moe_kernel* kernel) { delete kernel; }
+
+moe_status moe_kernel_set_profiling(moe_kernel* kernel, int32_t enable) {
+  if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+  if (enable && !kernel->ev[0]) {
+    for (auto& ev : kernel->ev) {
+      const hipError_t e = hipEventCreate(&ev);
+      if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    }
+  }
+  kernel->profiling = enable != 0;
+  kernel->ev_recorded = false;
+  return MOE_OK;
+}
+
+moe_status moe_kernel_stage_times(moe_kernel* kernel, float* ms, int32_t* path) {
+  if (!kernel || !ms) return fail(MOE_INVALID_ARGUMENT, "null argument");
+  if (!kernel->ev_recorded) return fail(MOE_INVALID_ARGUMENT, "no profiled call recorded");
+  hipError_t e = hipEventSynchronize(kernel->ev[4]);
+  if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+  for (int i = 0; i < 4; ++i) {
+    e = hipEventElapsedTime(&ms[i], kernel->ev[i], kernel->ev[i + 1]);
+    if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+  }
+  if (path) *path = kernel->last_path;
+  return MOE_OK;
+}
 
 const char* moe_last_error(void) { return g_last_error.c_str(); }
 

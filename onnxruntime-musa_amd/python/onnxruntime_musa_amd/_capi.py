@@ -88,6 +88,9 @@ EXPORTS = [
     ("moe_kernel_workspace_layout", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                                    ctypes.POINTER(MoeWorkspaceLayout)]),
     ("moe_kernel_set_expert_path", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    ("moe_kernel_set_profiling", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    ("moe_kernel_stage_times", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
+                                              ctypes.POINTER(ctypes.c_int32)]),
     ("moe_last_error", ctypes.c_char_p, []),
     ("moe_route_dispatch_scratch_size", ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     ("moe_route_dispatch_launch", ctypes.c_int, [ctypes.POINTER(MoeRouteParams), ctypes.c_void_p]),

@@ -98,6 +98,22 @@ class _MoEOp:
         arr = (MoeTensor * len(inputs))(*[_tensor_desc(t) for t in inputs])
         return arr, len(inputs)
 
+    def set_profiling(self, enable: bool = True) -> None:
+        check(self._lib.moe_kernel_set_profiling(self._h, int(enable)))
+
+    STAGES = ("route_dispatch", "fc1", "fc2", "finalize")
+    PATH_NAMES = ("simt", "decode", "prefill")
+
+    def stage_times(self) -> dict:
+        """Stage durations (ms) of the last profiled call, from HIP events
+        recorded on the call's stream; waits for that call to finish."""
+        ms = (ctypes.c_float * 4)()
+        path = ctypes.c_int32()
+        check(self._lib.moe_kernel_stage_times(self._h, ms, ctypes.byref(path)))
+        out = {n: float(ms[i]) for i, n in enumerate(self.STAGES)}
+        out["path"] = self.PATH_NAMES[path.value]
+        return out
+
     def workspace_size(self, *inputs) -> int:
         arr, n = self._descs(inputs)
         out = ctypes.c_size_t()
@@ -125,6 +141,23 @@ class _MoEOp:
         check(self._lib.moe_kernel_compute(self._h, arr, n, out.data_ptr() if out.numel() else None, ws_ptr,
                                            ws_bytes, ctypes.c_void_p(s.cuda_stream)))
         return out
+
+    def bind(self, *inputs, out: torch.Tensor, workspace: torch.Tensor,
+             stream: Optional[torch.cuda.Stream] = None):
+        """Pre-builds the C arguments for repeated calls on fixed buffers (a
+        serving loop); returns a zero-argument callable that enqueues one
+        invocation.  The tensors must stay alive while the callable is used."""
+        arr, n = self._descs(inputs)
+        s = stream if stream is not None else torch.cuda.current_stream(inputs[0].device)
+        fn = self._lib.moe_kernel_compute
+        args = (self._h, arr, n, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()),
+                workspace.numel() * workspace.element_size(), ctypes.c_void_p(s.cuda_stream))
+        keep = (inputs, out, workspace)
+
+        def call():
+            check(fn(*args))
+            return keep[1]
+        return call
 
 
 class MoE(_MoEOp):

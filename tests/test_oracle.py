@@ -1,0 +1,458 @@
+"""Pins the CPU oracle (oracle/moe_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something that does not restate it:
+
+  conversions  numpy's IEEE fp16 (exhaustive for fp16 -> fp32), known bf16 RNE
+               values, the reference's bf16 helper formula
+               (test/ops/op_test_utils.py:235-245)
+  orc_route    the reference's TopK known-answer vectors
+               (test/ops/test_topk.py:212-227, 230-246, 307-323), float64
+               closed-form softmax / sigmoid, k = E full order, normalised
+               k = 1 weight 1
+  orc_dispatch brute force (a stable sort by expert) on every routing of tiny
+               shapes, invariants on large random routings
+  orc_dequant  hand-packed bytes (0x80 -> 0 for int8; 0x78 -> 0, -1 for int4)
+               and block-boundary scale indexing
+  activations  closed forms at fixed points (SiLU, erf-GELU, clamped SwiGLU)
+  forward      an independent float64 numpy formulation (dense matmuls),
+               layout equivalences (fc1/fc3 unfused == fused chunked ==
+               fused interleaved), QMoE == MoE on dequantised weights,
+               single-expert == dense FFN, linearity in the fc2 scales
+  fixtures     tests/golden/*.npz written by tests/golden/make_golden.py
+
+The "planted mistake" tests feed each check a plausible mistake (swapped tie
+order, unstable dispatch, high-nibble-first decode, dropped bias, swapped
+gate/linear halves) on the CPU and assert that the check rejects it.
+"""
+import itertools
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- conversions
+def test_f16_to_f32_exhaustive():
+    lib = oracle.load()
+    bits = np.arange(65536, dtype=np.uint32)
+    got = np.array([lib.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    exp = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne():
+    lib = oracle.load()
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(100),
+        rng.standard_normal(5000).astype(np.float32) * np.float32(1e-5),   # fp16 subnormal range
+        np.array([65504, 65519.99, 65520, 65536, 1e-8, 5.96e-8, 2.98e-8, 2.99e-8, -0.0, np.inf, -np.inf],
+                 np.float32),
+        # exact halfway points between fp16 neighbours
+        (np.arange(1024, 1100, dtype=np.float32) + np.float32(0.5)),
+    ])
+    got = np.array([lib.orc_f32_to_f16(float(v)) for v in vals], np.uint16)
+    exp = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, exp)
+
+
+@pytest.mark.parametrize("f,bits", [(1.0, 0x3F80), (-2.0, 0xC000), (1.00390625, 0x3F80),
+                                    (1.01171875, 0x3F82), (3.0e38, 0x7F62)])
+def test_bf16_known_values(f, bits):
+    assert oracle.load().orc_f32_to_bf16(f) == bits
+    back = np.array([bits << 16], np.uint32).view(np.float32)[0]
+    assert np.float32(oracle.load().orc_bf16_to_f32(bits)) == back
+
+
+def test_bf16_matches_reference_helper():
+    lib = oracle.load()
+    rng = np.random.default_rng(1)
+    vals = rng.standard_normal(5000).astype(np.float32) * np.float32(7)
+    got = np.array([lib.orc_f32_to_bf16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, oracle.f32_to_bf16_bits(vals))
+
+
+# ---------------------------------------------------------------- router
+def test_topk_kat_ties_go_to_lower_index():
+    # test_topk.py:230-246 (k=1 along an axis with equal maxima)
+    ids, _ = oracle.route(np.array([[4.0, 7.0, 1.0, 7.0], [9.0, 1.0, 9.0, 8.0]]), 1)
+    assert ids[:, 0].tolist() == [1, 0]
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (4000, 128)])
+def test_topk_kat_all_equal_gives_arange(E, k):
+    # test_topk.py:307-323
+    ids, _ = oracle.route(np.full((2, E), 3.25, np.float32), k)
+    assert np.array_equal(ids, np.tile(np.arange(k), (2, 1)))
+
+
+def test_topk_kat_adjacent_floats_are_not_ties():
+    # test_topk.py:212-227
+    nxt = np.nextafter(np.float32(10.0), np.float32(np.inf))
+    ids, _ = oracle.route(np.array([[10.0, nxt, 9.0]], np.float32), 1)
+    assert ids.tolist() == [[1]]
+
+
+def test_route_k_equals_e_is_stable_argsort():
+    rng = np.random.default_rng(2)
+    lg = np.round(rng.standard_normal((50, 9)) * 2).astype(np.float32)  # many ties
+    ids, _ = oracle.route(lg, 9)
+    assert np.array_equal(ids, np.argsort(-lg, axis=1, kind="stable"))
+
+
+@pytest.mark.parametrize("normalize", [0, 1])
+def test_route_softmax_closed_form(normalize):
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal((200, 16)).astype(np.float32)
+    ids, w = oracle.route(lg, 4, normalize=bool(normalize))
+    l64 = lg.astype(np.float64)
+    p = np.exp(l64 - l64.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    sel = np.take_along_axis(p, ids, 1)
+    if normalize:
+        sel /= sel.sum(1, keepdims=True)
+    np.testing.assert_allclose(w, sel, rtol=1e-6)
+
+
+def test_route_sigmoid_closed_form():
+    rng = np.random.default_rng(4)
+    lg = rng.standard_normal((100, 8)).astype(np.float32)
+    ids, w = oracle.route(lg, 3, sigmoid=True)
+    np.testing.assert_allclose(w, 1 / (1 + np.exp(-np.take_along_axis(lg.astype(np.float64), ids, 1))), rtol=1e-6)
+
+
+def test_route_normalized_k1_weight_is_one():
+    rng = np.random.default_rng(5)
+    _, w = oracle.route(rng.standard_normal((40, 8)).astype(np.float32), 1, normalize=True)
+    assert np.all(w == 1.0)
+
+
+def test_route_nan_ranks_last():
+    lg = np.array([[np.nan, 1.0, -5.0, np.nan]], np.float32)
+    ids, _ = oracle.route(lg, 4)
+    assert ids.tolist() == [[1, 2, 0, 3]]
+
+
+def test_planted_tie_mistake_is_caught():
+    """A router that breaks ties toward the higher id fails the KAT."""
+    lg = np.array([[4.0, 7.0, 1.0, 7.0]], np.float32)
+    mutant = np.argsort(-lg[:, ::-1], axis=1, kind="stable")[:, :1]
+    mutant = lg.shape[1] - 1 - mutant
+    ids, _ = oracle.route(lg, 1)
+    assert mutant.tolist() == [[3]] and ids.tolist() == [[1]]
+
+
+# ---------------------------------------------------------------- dispatch
+def _brute_dispatch(ids, E):
+    flat = ids.reshape(-1)
+    perm = sorted(range(flat.size), key=lambda f: (flat[f], f))
+    offs = [0] + list(np.cumsum(np.bincount(flat, minlength=E)))
+    return np.array(offs, np.int32), np.array(perm, np.int32)
+
+
+def test_dispatch_brute_force_all_tiny_routings():
+    n = 0
+    for E, k, T in [(1, 1, 3), (2, 1, 3), (3, 2, 3), (4, 2, 3), (3, 3, 2)]:
+        choices = [c for c in itertools.permutations(range(E), k)]
+        for combo in itertools.product(choices, repeat=T):
+            ids = np.array(combo, np.int32).reshape(T, k)
+            offs, perm = oracle.dispatch(ids, E)
+            bo, bp = _brute_dispatch(ids, E)
+            assert np.array_equal(offs, bo) and np.array_equal(perm, bp)
+            n += 1
+    assert n == 1 + 8 + 216 + 1728 + 36
+
+
+def test_dispatch_invariants_large():
+    rng = np.random.default_rng(6)
+    T, k, E = 5000, 8, 128
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    offs, perm = oracle.dispatch(ids, E)
+    assert offs[0] == 0 and offs[-1] == T * k
+    assert np.array_equal(np.sort(perm), np.arange(T * k))          # bijection
+    assert np.array_equal(np.diff(offs), np.bincount(ids.reshape(-1), minlength=E))
+    flat = ids.reshape(-1)
+    for e in range(E):
+        rows = perm[offs[e]:offs[e + 1]]
+        assert np.all(flat[rows] == e) and np.all(np.diff(rows) > 0)  # ascending tokens
+
+
+def test_planted_unstable_dispatch_is_caught():
+    ids = np.array([[0, 1], [1, 0], [0, 2]], np.int32)
+    offs, perm = oracle.dispatch(ids, 3)
+    bo, bp = _brute_dispatch(ids, 3)
+    assert np.array_equal(perm, bp)
+    mutant = perm.copy()
+    mutant[offs[0]:offs[1]] = mutant[offs[0]:offs[1]][::-1]  # tokens descending inside expert 0
+    assert not np.array_equal(mutant, bp)
+
+
+# ---------------------------------------------------------------- dequant
+def test_dequant_int8_kat():
+    q = np.array([[0x80, 0xFF, 0x00, 0x81]], np.uint8)
+    s = np.array([0.5], np.float32)
+    np.testing.assert_array_equal(oracle.dequant(q, s, "f32", 8, 0, 1, 4), [[0.0, 63.5, -64.0, 0.5]])
+
+
+def test_dequant_int4_kat_low_nibble_first():
+    q = np.array([[0x78, 0x0F]], np.uint8)  # bytes -> k0=8, k1=7, k2=15, k3=0
+    s = np.array([2.0], np.float32)
+    np.testing.assert_array_equal(oracle.dequant(q, s, "f32", 4, 0, 1, 4), [[0.0, -2.0, 14.0, -16.0]])
+
+
+def test_planted_high_nibble_first_is_caught():
+    q = np.array([[0x78]], np.uint8)
+    s = np.array([1.0], np.float32)
+    got = oracle.dequant(q, s, "f32", 4, 0, 1, 2)
+    mutant = np.array([[(0x78 >> 4) - 8, (0x78 & 15) - 8]], np.float32)
+    assert got.tolist() == [[0.0, -1.0]] and not np.array_equal(got, mutant)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequant_block_scale_indexing(bits):
+    K, bs = 64, 16
+    nbytes = K // 2 if bits == 4 else K
+    q = np.full((2, nbytes), 0x99 if bits == 4 else 0x81, np.uint8)  # every element decodes to +1
+    s = (np.arange(2 * K // bs, dtype=np.float32) + 1).reshape(2, K // bs)
+    got = oracle.dequant(q, s, "f32", bits, bs, 2, K)
+    exp = np.repeat(s, bs, axis=1)
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_dequant_f16_scales():
+    q = np.array([[0x82]], np.uint8)
+    s = np.array([0.1], np.float16)
+    got = oracle.dequant(q, s, "f16", 8, 0, 1, 1)
+    assert got[0, 0] == np.float32(2.0) * np.float32(np.float16(0.1))
+
+
+# ---------------------------------------------------------------- activations
+def test_activation_closed_forms():
+    h = np.array([1.0, -2.0, 0.5], np.float32)
+    np.testing.assert_allclose(oracle.activation(h, None, 3, "silu"), h / (1 + np.exp(-h)), rtol=1e-6)
+    erf = np.vectorize(math.erf)
+    np.testing.assert_allclose(oracle.activation(h, None, 3, "gelu"), 0.5 * h * (1 + erf(h / math.sqrt(2))),
+                               rtol=1e-6)
+    np.testing.assert_array_equal(oracle.activation(h, None, 3, "relu"), [1.0, 0.0, 0.5])
+    np.testing.assert_array_equal(oracle.activation(h, None, 3, "identity"), h)
+    assert abs(oracle.activation(np.array([1.0], np.float32), None, 1, "silu")[0] - 0.7310585786300049) < 1e-7
+
+
+def test_swiglu_layouts_and_clamp():
+    g = np.array([10.0, -1.0], np.float32)
+    l = np.array([-10.0, 2.0], np.float32)
+    alpha, beta, lim = 1.702, 1.0, 7.0
+
+    def ref(g, l):
+        G = np.minimum(g, lim)
+        L = np.clip(l, -lim, lim)
+        return G / (1 + np.exp(-alpha * G)) * (L + beta)
+
+    inter = np.stack([g, l], 1).reshape(-1)
+    chunk = np.concatenate([g, l])
+    np.testing.assert_allclose(oracle.activation(inter, None, 2, "swiglu", 1, alpha, beta, lim), ref(g, l), rtol=1e-6)
+    np.testing.assert_allclose(oracle.activation(chunk, None, 2, "swiglu", 2, alpha, beta, lim), ref(g, l), rtol=1e-6)
+    np.testing.assert_allclose(oracle.activation(g, l, 2, "swiglu", 0, alpha, beta, lim), ref(g, l), rtol=1e-6)
+    # SiLU gating with fc3
+    np.testing.assert_allclose(oracle.activation(g, l, 2, "silu"), g / (1 + np.exp(-g)) * l, rtol=1e-6)
+
+
+def test_planted_swapped_gate_linear_is_caught():
+    g = np.array([3.0], np.float32)
+    l = np.array([-0.5], np.float32)
+    good = oracle.activation(np.array([3.0, -0.5], np.float32), None, 1, "swiglu", 1)
+    swapped = oracle.activation(np.array([-0.5, 3.0], np.float32), None, 1, "swiglu", 1)
+    assert np.isclose(good[0], 3.0 / (1 + math.exp(-3.0)) * -0.5) and not np.isclose(good[0], swapped[0])
+
+
+# ---------------------------------------------------------------- forward
+def _np64_forward(cfg, h):
+    """Independent float64 formulation with dense matmuls over all tokens."""
+    T = h["input"].shape[0]
+    x = oracle.to_f32(h["input"], cfg.dtype).astype(np.float64)
+    lg = oracle.to_f32(h["router_probs"], cfg.dtype).astype(np.float64)
+    p = np.exp(lg - lg.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    order = np.argsort(-lg, axis=1, kind="stable")[:, :cfg.k]
+    w = np.take_along_axis(p, order, 1)
+    if cfg.normalize:
+        w /= w.sum(1, keepdims=True)
+
+    def mat(name, sname, N, K):
+        q = h.get(name)
+        if q is None:
+            return None
+        if cfg.bits == 0:
+            return oracle.to_f32(q, cfg.dtype).astype(np.float64)
+        return np.stack([oracle.dequant(q[e], h[sname][e], cfg.scale_dtype, cfg.bits, cfg.block_size, N, K)
+                         for e in range(cfg.experts)]).astype(np.float64)
+
+    def vec(name):
+        return None if h.get(name) is None else oracle.to_f32(h[name], cfg.dtype).astype(np.float64)
+
+    W1 = mat("fc1_experts_weights", "fc1_scales", cfg.n1, cfg.hidden)
+    W2 = mat("fc2_experts_weights", "fc2_scales", cfg.hidden, cfg.inter)
+    W3 = mat("fc3_experts_weights", "fc3_scales", cfg.inter, cfg.hidden)
+    b1, b2, b3 = vec("fc1_experts_bias"), vec("fc2_experts_bias"), vec("fc3_experts_bias")
+    sig = lambda v: 1 / (1 + np.exp(-v))  # noqa: E731
+    lim = np.inf if cfg.swiglu_limit is None else cfg.swiglu_limit
+    out = np.zeros((T, cfg.hidden))
+    for e in range(cfg.experts):
+        tok, slot = np.nonzero(order == e)
+        if tok.size == 0:
+            continue
+        h1 = x[tok] @ W1[e].T + (0 if b1 is None else b1[e])
+        if W3 is not None:
+            h3 = x[tok] @ W3[e].T + (0 if b3 is None else b3[e])
+            g, l = h1, h3
+        elif cfg.activation == "swiglu":
+            g, l = (h1[:, 0::2], h1[:, 1::2]) if cfg.swiglu_fusion == 1 else (h1[:, :cfg.inter], h1[:, cfg.inter:])
+        else:
+            g, l = h1, None
+        if cfg.activation == "swiglu":
+            G = np.minimum(g, lim)
+            a = G * sig(cfg.alpha * G) * (np.clip(l, -lim, lim) + cfg.beta)
+        else:
+            a = {"silu": g * sig(g), "relu": np.maximum(g, 0), "identity": g}[cfg.activation]
+            if l is not None:
+                a = a * l
+        y = a @ W2[e].T + (0 if b2 is None else b2[e])
+        out[tok] += w[tok, slot][:, None] * y
+    return out
+
+
+def _problem(name, T=24, seed=1, **over):
+    from onnxruntime_musa_amd.workloads import CONFIGS, make_problem, to_host
+    p = make_problem(CONFIGS[name], T, seed=seed, device="cpu", gen="numpy", **over)
+    return p.cfg, {n: to_host(t) for n, t in p.inputs.items()}
+
+
+FORWARD_CASES = [
+    ("c1_moe_f32", {}),
+    ("c2_qmoe_int8_mixtral", dict(hidden=128, inter=256)),
+    ("c3_qmoe_int4_mixtral", dict(hidden=128, inter=256)),
+    ("c4_qmoe_int4_gptoss", dict(hidden=128, inter=192, experts=8)),
+    ("c5_moe_f16_qwen3", dict(hidden=128, inter=64, experts=16, k=4)),
+    ("c3_qmoe_int4_mixtral", dict(hidden=128, inter=256, use_fc3=False, swiglu_fusion=2, bias=True)),
+    ("c1_moe_f32", dict(activation="relu", normalize=0)),
+    ("c1_moe_f32", dict(activation="silu", use_fc3=True, bias=True)),
+]
+
+
+@pytest.mark.parametrize("name,over", FORWARD_CASES)
+def test_forward_matches_float64_formulation(name, over):
+    cfg, h = _problem(name, **over)
+    r = oracle.forward_problem(cfg, h)
+    ref = _np64_forward(cfg, h)
+    np.testing.assert_allclose(r["out_f32"], ref, rtol=1e-5, atol=2e-6)
+
+
+def test_planted_dropped_bias_is_caught():
+    cfg, h = _problem("c1_moe_f32")
+    ref = _np64_forward(cfg, h)
+    h2 = dict(h)
+    h2["fc2_experts_bias"] = None
+    bad = oracle.forward_problem(cfg, h2)["out_f32"]
+    assert np.max(np.abs(bad - ref)) > 1e-3
+
+
+def test_unfused_equals_fused_layouts():
+    from dataclasses import replace
+    cfg, h = _problem("c1_moe_f32", activation="swiglu", use_fc3=True, bias=True)
+    base = oracle.forward_problem(cfg, h)["out_f32"]
+    W1, W3 = h["fc1_experts_weights"], h["fc3_experts_weights"]
+    b1, b3 = h["fc1_experts_bias"], h["fc3_experts_bias"]
+    chunk = dict(h, fc1_experts_weights=np.concatenate([W1, W3], 1), fc1_experts_bias=np.concatenate([b1, b3], 1),
+                 fc3_experts_weights=None, fc3_experts_bias=None)
+    inter_w = np.stack([W1, W3], 2).reshape(W1.shape[0], -1, W1.shape[2])
+    inter_b = np.stack([b1, b3], 2).reshape(b1.shape[0], -1)
+    inter = dict(chunk, fc1_experts_weights=inter_w, fc1_experts_bias=inter_b)
+    c2 = oracle.forward_problem(replace(cfg, use_fc3=False, swiglu_fusion=2), chunk)["out_f32"]
+    c1 = oracle.forward_problem(replace(cfg, use_fc3=False, swiglu_fusion=1), inter)["out_f32"]
+    np.testing.assert_array_equal(base, c2)
+    np.testing.assert_array_equal(base, c1)
+
+
+@pytest.mark.parametrize("name", ["c2_qmoe_int8_mixtral", "c3_qmoe_int4_mixtral"])
+def test_qmoe_equals_moe_on_dequantised_weights(name):
+    from dataclasses import replace
+    cfg, h = _problem(name, hidden=128, inter=256, dtype="f32", scale_dtype="f32")
+    q = oracle.forward_problem(cfg, h)["out_f32"]
+    deq = {}
+    for w, s, N, K in [("fc1_experts_weights", "fc1_scales", cfg.n1, cfg.hidden),
+                       ("fc2_experts_weights", "fc2_scales", cfg.hidden, cfg.inter),
+                       ("fc3_experts_weights", "fc3_scales", cfg.inter, cfg.hidden)]:
+        deq[w] = np.stack([oracle.dequant(h[w][e], h[s][e], "f32", cfg.bits, cfg.block_size, N, K)
+                           for e in range(cfg.experts)])
+    dense = {n: v for n, v in h.items() if not n.endswith("scales")}
+    dense.update(deq)
+    m = oracle.forward_problem(replace(cfg, bits=0, block_size=0), dense)["out_f32"]
+    np.testing.assert_array_equal(q, m)
+
+
+def test_single_expert_is_dense_ffn():
+    cfg, h = _problem("c1_moe_f32", experts=1, k=1, activation="silu")
+    r = oracle.forward_problem(cfg, h)
+    x = h["input"].astype(np.float64)
+    a = x @ h["fc1_experts_weights"][0].T.astype(np.float64) + h["fc1_experts_bias"][0]
+    a = a / (1 + np.exp(-a))
+    y = a @ h["fc2_experts_weights"][0].T.astype(np.float64) + h["fc2_experts_bias"][0]
+    np.testing.assert_allclose(r["out_f32"], y, rtol=1e-5, atol=2e-6)
+    assert np.all(r["topk_w"] == 1.0)
+
+
+def test_linear_in_fc2_scales():
+    cfg, h = _problem("c2_qmoe_int8_mixtral", hidden=128, inter=128, dtype="f32", scale_dtype="f32")
+    a = oracle.forward_problem(cfg, h)["out_f32"]
+    h2 = dict(h, fc2_scales=h["fc2_scales"] * np.float32(2.0))
+    b = oracle.forward_problem(cfg, h2)["out_f32"]
+    np.testing.assert_allclose(b, 2 * a, rtol=1e-6, atol=1e-7)
+
+
+def test_token_mask_computes_only_masked_rows():
+    cfg, h = _problem("c1_moe_f32", T=20)
+    full = oracle.forward_problem(cfg, h)["out_f32"]
+    mask = np.zeros(20, np.uint8)
+    mask[[3, 7, 19]] = 1
+    part = oracle.forward_problem(cfg, h, token_mask=mask)["out_f32"]
+    np.testing.assert_array_equal(part[[3, 7, 19]], full[[3, 7, 19]])
+
+
+def test_thread_count_does_not_change_results():
+    cfg, h = _problem("c3_qmoe_int4_mixtral", hidden=128, inter=256)
+    a = oracle.forward_problem(cfg, h, threads=1)["out_f32"]
+    b = oracle.forward_problem(cfg, h, threads=4)["out_f32"]
+    np.testing.assert_array_equal(a, b)
+
+
+# ---------------------------------------------------------------- fixtures
+def test_golden_c1_fixture():
+    """configs[0] (fp32 MoE, 64 tokens) from its seed: oracle output and routing
+    equal the committed fixture."""
+    fx = np.load(GOLDEN / "c1_moe_f32_seed0.npz", allow_pickle=False)
+    cfg, h = _problem("c1_moe_f32", T=int(fx["tokens"]), seed=int(fx["seed"]))
+    np.testing.assert_array_equal(h["input"].reshape(-1)[:16], fx["input_head"])
+    r = oracle.forward_problem(cfg, h)
+    np.testing.assert_array_equal(r["topk_ids"], fx["topk_ids"])
+    np.testing.assert_array_equal(r["perm"], fx["perm"])
+    np.testing.assert_allclose(r["out_f32"], fx["out"], rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("fixture", sorted(p.name for p in GOLDEN.glob("qmoe_*.npz")))
+def test_golden_qmoe_fixtures(fixture):
+    from onnxruntime_musa_amd.workloads import CONFIGS
+    fx = np.load(GOLDEN / fixture, allow_pickle=False)
+    name = str(fx["config"])
+    over = {k: int(fx[k]) for k in ("hidden", "inter", "experts")}
+    cfg, h = _problem(name, T=int(fx["tokens"]), seed=int(fx["seed"]), **over)
+    assert cfg.bits == CONFIGS[name].bits
+    r = oracle.forward_problem(cfg, h)
+    np.testing.assert_array_equal(r["topk_ids"], fx["topk_ids"])
+    np.testing.assert_allclose(r["out_f32"], fx["out"], rtol=0, atol=1e-6)
