@@ -12,8 +12,9 @@
 // What bounds this kernel is the vector-memory path (address unit and L1
 // tag lookups per byte), not HBM, so the design minimises L1 accesses per
 // weight byte:
-//   * each wave owns WT weight tiles (up to 8 x 16 rows), so one activation
-//     fragment is reused by WT MFMAs;
+//   * each wave owns WT = 2 weight tiles (16 rows each), so one activation
+//     fragment is reused by 2 MFMAs (more tiles per wave cut parallelism
+//     more than they save);
 //   * all loads are raw buffer loads; absent tokens, features past the end
 //     and the missing part of a partial last chunk use an out-of-range
 //     offset, which returns zero without any memory access;
@@ -80,7 +81,7 @@ template <int WF, int NG, bool GATED>
 struct Geo {
   static constexpr int kVecs = WF == kInt4 ? 1 : (WF == kInt8 ? 2 : 4);  // u32x4 per tile per chunk
   static constexpr int kLaneBytes = 16 * kVecs;                           // bytes per 32 k of a row
-  static constexpr int WT = NG == 1 ? (WF == kInt4 ? 8 : (WF == kInt8 ? 4 : 2)) : 2;  // weight tiles
+  static constexpr int WT = 2;  // weight tiles (gate + linear of 16 features, or 2 x 16 features)
   static constexpr int FT = GATED ? WT / 2 : WT;                                       // feature tiles
   static constexpr int kChunkVgprs = WT * 4 * kVecs + 16 * NG;
   static constexpr int PD = kChunkVgprs <= 64 ? 3 : 2;
@@ -393,10 +394,7 @@ inline int scale_mode(const ExpertArgs& a) {
 }
 
 // Host mirror of Geo<>: weight tiles per wave.
-inline int weight_tiles(int wfmt, int64_t T) {
-  if (T > 16) return 2;
-  return wfmt == kInt4 ? 8 : (wfmt == kInt8 ? 4 : 2);
-}
+inline int weight_tiles(int /*wfmt*/, int64_t /*T*/) { return 2; }
 
 // Quantised formats: dispatch over activation type, scale mode and scale type.
 template <int WF>

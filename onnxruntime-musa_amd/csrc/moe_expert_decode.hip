@@ -97,10 +97,14 @@ DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, in
   const bool gated = gate_mode != kGateNone;
   pl.y2_planes_max = kMaxDecodeKsplit;
   if (T > kLdsMaxTokens) return pl;
-  pl.lds = true;
   const int64_t e_act = std::min<int64_t>(E, T * k);
   const int64_t ft1 = gated ? 1 : 2, ft2 = 2;
   pl.fgroups1 = static_cast<int32_t>((I + 64 * ft1 - 1) / (64 * ft1));
+  // fc1 cannot split K across workgroups, so it stages activations in LDS
+  // only when its feature groups alone give at least one workgroup per CU;
+  // fc2 splits K as needed.
+  pl.lds = e_act * pl.fgroups1 >= 256;
+  pl.lds2 = true;
   const int64_t fgroups2 = (H + 64 * ft2 - 1) / (64 * ft2);
   decode::lds_groups(H, pl.fgroups1, e_act, false, &pl.ksg1, &pl.kr1);
   decode::lds_groups(I, fgroups2, e_act, true, &pl.ksg2, &pl.kr2);
@@ -209,7 +213,7 @@ hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
 hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream) {
   decode::Stage st = fc2_stage(a);
   const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
-  if (pl.lds) {
+  if (pl.lds2) {
     decode::LdsStage ls{};
     ls.s = st;
     ls.s.ks = 1;

@@ -72,7 +72,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
   const int nchunks = static_cast<int>((K + kChunk - 1) / kChunk);
   const int cper = ls.kr / kChunk;
   const int c0 = static_cast<int>(blockIdx.z) * cper;
-  const int c1 = c0 + cper < nchunks ? c0 + cper : nchunks;
+  const int c1 = c0 + cper < nchunks ? c0 + cper : nchunks;  // real chunks [c0, c1)
   const int64_t ktail = K - static_cast<int64_t>(nchunks - 1) * kChunk;
 
   // ---- weights: tile rows and buffer offsets ----
@@ -93,7 +93,8 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
 
   using CK = LChunk<WF, GATED>;
   auto fetch = [&](int c, CK& d) {
-    const bool kin = c < nchunks - 1 || 32 * g + 32 <= ktail;
+    // padding chunks past K and the missing lanes of a partial last chunk read nothing
+    const bool kin = c < nchunks - 1 || (c == nchunks - 1 && 32 * g + 32 <= ktail);
     const uint32_t wc = static_cast<uint32_t>(c) * (4 * LB);
 #pragma unroll
     for (int t = 0; t < WT; ++t) {
@@ -143,12 +144,13 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
 
   // Start the weight stream before staging, so the first chunks are in flight
   // while the first activation piece is copied.
+  // The K range is walked in whole pieces of PC chunks; chunks past c1 are
+  // padding that reads nothing and multiplies zeros.
+  const int npieces = (c1 - c0 + PC - 1) / PC;
+  const int cend = c0 + npieces * PC;
   CK ring[PD];
-  const int clast = c1 - 1;
-  if (c0 < c1) {
 #pragma unroll
-    for (int d = 0; d < PD; ++d) fetch(min(c0 + d, clast), ring[d]);
-  }
+  for (int d = 0; d < PD; ++d) fetch(c0 + d, ring[d]);
   xload(0);
 
   // ---- stage this wave's block scales: sc[(t * nb + b) * 16 + col] ----
@@ -159,24 +161,19 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
     bshift = __builtin_ctzll(static_cast<uint64_t>(p.block_size));
     const int64_t nblk = K / p.block_size;
     b0 = (static_cast<int64_t>(c0) * kChunk) >> bshift;
-    if (c1 > c0) {
-      const int64_t klast = std::min<int64_t>(static_cast<int64_t>(c1) * kChunk, K) - 1;
-      nb = static_cast<int>((klast >> bshift) + 1 - b0);
-    }
+    nb = static_cast<int>(((static_cast<int64_t>(cend) * kChunk - 1) >> bshift) + 1 - b0);
     const typename ST::storage* sgp = static_cast<const typename ST::storage*>(p.s);
     const typename ST::storage* slp = static_cast<const typename ST::storage*>(p.sl);
-    for (int i = lane; i < WT * 16 * nb; i += kWave) {
-      const int b = i % nb, tc = i / nb;
-      const int t = tc / 16, cc = tc % 16;
-      const bool lin = GATED && t >= FT;
-      const int64_t f = fbase + (t % FT) * 16 + cc;
-      float v = 0.0f;
-      if (f < p.nfeat) {
-        const int64_t r = tile_row(f, lin, FC1 && GATED, p.gate_mode, p.nfeat);
-        const int64_t rows = lin ? p.wl_rows : p.w_rows;
-        v = to_f32<ST>((lin ? slp : sgp)[(static_cast<int64_t>(e) * rows + r) * nblk + b0 + b]);
-      }
-      sc[(t * nb + b) * 16 + cc] = v;
+    // lane -> (tile, row) pair; the two lane halves take alternate blocks
+    const int pair = lane & 31, t = pair >> 4, cc = pair & 15;
+    const bool lin = GATED && t >= FT;
+    const int64_t f = fbase + (t % FT) * 16 + cc;
+    const int64_t r = tile_row(f < p.nfeat ? f : 0, lin, FC1 && GATED, p.gate_mode, p.nfeat);
+    const typename ST::storage* srow =
+        (lin ? slp : sgp) + (static_cast<int64_t>(e) * (lin ? p.wl_rows : p.w_rows) + r) * nblk;
+    for (int b = lane >> 5; b < nb; b += 2) {
+      const bool ok = f < p.nfeat && b0 + b < nblk;
+      sc[(t * nb + b) * 16 + cc] = ok ? to_f32<ST>(srow[b0 + b]) : 0.0f;
     }
   }
   xstore(0);
@@ -185,7 +182,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
   floatx4_t acc[WT];
 #pragma unroll
   for (int t = 0; t < WT; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  const bool xrow_ok = col < nrows;
+  const int b0i = static_cast<int>(b0);  // K < 2^31: block indices fit 32 bits
 
   auto compute = [&](int c, int buf, int cin, const CK& d) {
     floatx4_t tmp[WT];
@@ -194,12 +191,14 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
     const uint8_t* xc = smem + buf * G::kBuf + col * G::kPitch + g * 64 + cin * (kChunk * 2);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4_t a = xrow_ok ? *reinterpret_cast<const u32x4_t*>(xc + 16 * s) : u32x4_t{0u, 0u, 0u, 0u};
+      // rows past the expert's token count hold stale data; they only feed
+      // output rows that are never stored
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xc + 16 * s);
 #pragma unroll
       for (int t = 0; t < WT; ++t) {
         float fs = 0.0f;
         if constexpr (SM == kScaleFold) {
-          const int blk = static_cast<int>(((static_cast<int64_t>(c) * kChunk + 32 * g + 8 * s) >> bshift) - b0);
+          const int blk = ((c * kChunk + 32 * g + 8 * s) >> bshift) - b0i;
           fs = sc[(t * nb + blk) * 16 + col];
         }
         const u32x4_t bw = weight_operand<AT, WF, SM == kScaleFold>(d.w[t], s, fs);
@@ -208,7 +207,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
       }
     }
     if constexpr (SM == kScaleBlock) {
-      const int blk = static_cast<int>(((static_cast<int64_t>(c) * kChunk) >> bshift) - b0);
+      const int blk = ((c * kChunk) >> bshift) - b0i;
 #pragma unroll
       for (int t = 0; t < WT; ++t) acc[t] += tmp[t] * sc[(t * nb + blk) * 16 + col];
     }
@@ -216,23 +215,17 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
 
   // Pieces of PC = PD chunks: piece q uses LDS buffer q % 2 and ring slots
   // 0..PC-1; the next piece's activations are loaded during the piece and
-  // stored behind it, then one barrier closes the piece.  The loop body has no
-  // data-dependent branches except the final partial piece.
-  const int npieces = (c1 - c0 + PC - 1) / PC;
+  // stored behind it, then one barrier closes the piece.
   for (int q = 0; q < npieces; ++q) {
     const int cq = c0 + q * PC;
     const bool more = q + 1 < npieces;
     if (more) xload(q + 1);
-    if (cq + PC <= c1) {
 #pragma unroll
-      for (int d = 0; d < PC; ++d) {
-        compute(cq + d, q & 1, d, ring[d]);
-        fetch(min(cq + d + PD, clast), ring[d]);
-      }
-    } else {
-#pragma unroll
-      for (int d = 0; d < PC; ++d)
-        if (cq + d < c1) compute(cq + d, q & 1, d, ring[d]);
+    for (int d = 0; d < PC; ++d) {
+      compute(cq + d, q & 1, d, ring[d]);
+      fetch(min(cq + d + PD, cend - 1), ring[d]);
+      // keep each chunk's LDS reads and dequantisation next to its MFMAs
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (more) xstore((q + 1) & 1);
     __syncthreads();

@@ -97,7 +97,8 @@ constexpr int kMaxDecodeKsplit = 8;
 // Launch plan of the decode kernels, shared by the workspace planner and the
 // launchers so both agree on the partial-plane sizes.
 struct DecodePlan {
-  bool lds = false;         // activation slice staged in LDS (T <= kLdsMaxTokens)
+  bool lds = false;         // fc1: activation slice staged in LDS
+  bool lds2 = false;        // fc2: activation slice staged in LDS
   int32_t ksg1 = 1, kr1 = 0, fgroups1 = 0;  // fc1 K groups, K per group, feature groups
   int32_t ksg2 = 1, kr2 = 0;                // fc2 K groups, K per group
   int64_t fc1_part_floats = 0;              // partial-plane storage of fc1
