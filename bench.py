@@ -77,6 +77,17 @@ def kernel_cost(cfg, T: int, hit: int):
                 layer_bytes=layer_bytes, layer_flops=fc1_flops + fc2_flops)
 
 
+def measured_traffic(key: str):
+    """HBM bytes per fc1 launch measured by two rocprofv3 PMC runs (FETCH_SIZE,
+    WRITE_SIZE), each scaled by what the counter reads for a plain copy of
+    known size; stored in profiles/traffic.json.  None when not measured."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    ent = json.loads(f.read_text()).get("workloads", {}).get(key)
+    return ent["bytes"] if ent else None
+
+
 def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=False):
     import torch
 
@@ -116,14 +127,15 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
     st = {k: statistics.mean(s[k] for s in stages) for k in ("route_dispatch", "fc1", "fc2", "finalize")}
     cost = kernel_cost(cfg, T, hit)
     decode = path != "prefill"
+    traffic = measured_traffic(f"{name}:{T}")
     if decode:
         fc1_ach = cost["fc1_bytes"] / (st["fc1"] * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=round(fc1_ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(fc1_ach / PEAK_HBM_GBS, 4), traffic=None)
+                    frac=round(fc1_ach / PEAK_HBM_GBS, 4), traffic=traffic)
     else:
         fc1_ach = cost["fc1_flops"] / (st["fc1"] * 1e-3) / 1e12
         roof = dict(bound="mfma", achieved=round(fc1_ach, 1), peak=PEAK_MFMA_TFLOPS, unit="TFLOP/s",
-                    frac=round(fc1_ach / PEAK_MFMA_TFLOPS, 4), traffic=None)
+                    frac=round(fc1_ach / PEAK_MFMA_TFLOPS, 4), traffic=traffic)
     layer_s = ms_per_step * 1e-3
     res = dict(workload=name, tokens=T, path=path, ms_per_step=round(ms_per_step, 4),
                tokens_per_s=round(T / layer_s, 1), experts_hit=hit,

@@ -135,10 +135,15 @@ MOE_API void moe_kernel_release(moe_kernel *kernel);
 
 /* Byte offsets, inside a caller-provided workspace, of the routing results a
  * moe_kernel_compute call leaves there (int32 topk_ids[T*k], float
- * topk_w[T*k], int32 offsets[E+1], int32 perm[T*k], int32 inv_perm[T*k]).
+ * topk_w[T*k], int32 offsets[E+1], int32 perm[T*k], int32 inv_perm[T*k]) and
+ * of the stage intermediates: act[T*k, I] (fc1/fc3 + activation output, input
+ * type, rows in dispatch order) and y2[y2_planes_max][T*k, H] (fp32 fc2
+ * partial sums over K ranges, bias in plane 0, rows in dispatch order; planes
+ * a call does not use are left untouched).
  * Library extension for parity tests; no reference counterpart. */
 typedef struct moe_workspace_layout {
   size_t topk_ids, topk_w, offsets, perm, inv_perm, total;
+  size_t act, y2, y2_planes_max;
 } moe_workspace_layout;
 MOE_API moe_status moe_kernel_workspace_layout(const moe_kernel *kernel, const moe_tensor *inputs,
                                        int32_t num_inputs, moe_workspace_layout *out);

@@ -176,10 +176,9 @@ __global__ void __launch_bounds__(256) gemv_kernel(Stage p) {
     bshift = __builtin_ctzll(static_cast<uint64_t>(p.block_size));
     const int64_t nblk = K / p.block_size;
     b0 = (static_cast<int64_t>(c0) * kChunk) >> bshift;
-    if (c1 > c0) {
-      const int64_t klast = std::min<int64_t>(static_cast<int64_t>(c1) * kChunk, K) - 1;
-      nb = static_cast<int>((klast >> bshift) + 1 - b0);
-    }
+    // whole chunks: the lanes of a partial last chunk that lie past K still
+    // read a scale (and multiply zeros), so their blocks are staged as 0
+    if (c1 > c0) nb = static_cast<int>(((static_cast<int64_t>(c1) * kChunk - 1) >> bshift) + 1 - b0);
     const typename ST::storage* sgp = static_cast<const typename ST::storage*>(p.s);
     const typename ST::storage* slp = static_cast<const typename ST::storage*>(p.sl);
     const int total = WT * 16 * nb;
@@ -189,7 +188,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(Stage p) {
       const bool lin = GATED && t >= FT;
       const int64_t f = fbase + (t % FT) * 16 + cc;
       float v = 0.0f;
-      if (f < p.nfeat) {
+      if (f < p.nfeat && b0 + b < nblk) {
         const int64_t r = tile_row(f, lin, FC1 && GATED, p.gate_mode, p.nfeat);
         const int64_t rows = lin ? p.wl_rows : p.w_rows;
         v = to_f32<ST>((lin ? slp : sgp)[(static_cast<int64_t>(e) * rows + r) * nblk + b0 + b]);

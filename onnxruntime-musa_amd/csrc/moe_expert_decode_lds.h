@@ -191,8 +191,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
     const uint8_t* xc = smem + buf * G::kBuf + col * G::kPitch + g * 64 + cin * (kChunk * 2);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      // rows past the expert's token count hold stale data; they only feed
-      // output rows that are never stored
+      // rows past the expert's token count were staged as zeros
       const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xc + 16 * s);
 #pragma unroll
       for (int t = 0; t < WT; ++t) {

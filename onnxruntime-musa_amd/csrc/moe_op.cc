@@ -416,6 +416,9 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
     out->perm = l.perm;
     out->inv_perm = l.inv_perm;
     out->total = l.total;
+    out->act = l.act;
+    out->y2 = l.y2;
+    out->y2_planes_max = static_cast<size_t>(std::max<int32_t>(l.decode.y2_planes_max, 1));
     return MOE_OK;
   } catch (const std::exception& e) {
     return fail(MOE_FAIL, e.what());

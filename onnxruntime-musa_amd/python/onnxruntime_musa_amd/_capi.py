@@ -51,7 +51,8 @@ class MoeTensor(ctypes.Structure):
 
 
 class MoeWorkspaceLayout(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_size_t) for n in ("topk_ids", "topk_w", "offsets", "perm", "inv_perm", "total")]
+    _fields_ = [(n, ctypes.c_size_t) for n in ("topk_ids", "topk_w", "offsets", "perm", "inv_perm", "total",
+                                               "act", "y2", "y2_planes_max")]
 
 
 class MoeRouteParams(ctypes.Structure):
