@@ -16,6 +16,7 @@
 #pragma once
 
 #include "moe_device.h"
+#include "moe_launch.h"
 
 namespace moe {
 
@@ -162,6 +163,43 @@ template <>
 __device__ __forceinline__ floatx16_t mfma32x32x16<BF16>(u32x4_t a, u32x4_t b, floatx16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+
+// ---- raw buffer access ----
+// Offset past every buffer range: a raw buffer load there returns 0 and makes
+// no memory access.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
+// Weight operand of MFMA step s from a lane's 16-byte weight vectors: the
+// 8 k of step s as 16-bit values (FOLD: times sc; otherwise exact integers).
+template <typename AT, int WF, bool FOLD>
+__device__ __forceinline__ u32x4_t weight_operand(const u32x4_t* v, int s, float sc) {
+  if constexpr (WF == kInt4) {
+    if constexpr (FOLD) return dq4_scaled<AT>(v[0][s], sc);
+    else return dq4_exact<AT>(v[0][s]);
+  } else if constexpr (WF == kInt8) {
+    const uint32_t a = v[s >> 1][(s & 1) * 2], b = v[s >> 1][(s & 1) * 2 + 1];
+    if constexpr (FOLD) return dq8_scaled<AT>(a, b, sc);
+    else return dq8_exact<AT>(a, b);
+  } else {
+    return v[s];
+  }
+}
+
+// Weight row (within one expert) that tile t of feature f reads.
+__device__ __forceinline__ int64_t tile_row(int64_t f, bool lin, bool fc1_gated, int gate_mode, int64_t nfeat) {
+  if (fc1_gated && gate_mode == kGateInterleaved) return 2 * f + (lin ? 1 : 0);
+  if (fc1_gated && gate_mode == kGateChunked) return f + (lin ? nfeat : 0);
+  return f;
 }
 
 }  // namespace moe

@@ -48,7 +48,6 @@ namespace moe {
 namespace decode {
 
 constexpr int kChunk = 128;             // K elements per lane-group pass
-constexpr uint32_t kOob = 0x80000000u;  // buffer offset past every range: reads 0, no access
 
 enum ScaleMode : int { kScaleNone = 0, kScaleChan = 1, kScaleBlock = 2, kScaleFold = 3 };
 
@@ -87,29 +86,6 @@ struct Geo {
   static constexpr int PD = kChunkVgprs <= 64 ? 3 : 2;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
-}
-__device__ __forceinline__ u32x4_t bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
-}
-
-// Weight operand of MFMA step s (0..3) from a tile's chunk vectors.
-template <typename AT, int WF, bool FOLD>
-__device__ __forceinline__ u32x4_t weight_operand(const u32x4_t* v, int s, float sc) {
-  if constexpr (WF == kInt4) {
-    if constexpr (FOLD) return dq4_scaled<AT>(v[0][s], sc);
-    else return dq4_exact<AT>(v[0][s]);
-  } else if constexpr (WF == kInt8) {
-    const uint32_t a = v[s >> 1][(s & 1) * 2], b = v[s >> 1][(s & 1) * 2 + 1];
-    if constexpr (FOLD) return dq8_scaled<AT>(a, b, sc);
-    else return dq8_exact<AT>(a, b);
-  } else {
-    return v[s];
-  }
-}
-
 template <int WF, int NG, bool GATED>
 struct Chunk {
   using G = Geo<WF, NG, GATED>;
@@ -117,12 +93,6 @@ struct Chunk {
   u32x4_t x[NG][4];
 };
 
-// Weight row (within one expert) that tile t of feature f reads.
-__device__ __forceinline__ int64_t tile_row(int64_t f, bool lin, bool fc1_gated, int gate_mode, int64_t nfeat) {
-  if (fc1_gated && gate_mode == kGateInterleaved) return 2 * f + (lin ? 1 : 0);
-  if (fc1_gated && gate_mode == kGateChunked) return f + (lin ? nfeat : 0);
-  return f;
-}
 
 template <typename AT, int WF, int SM, typename ST, int NG, bool FC1, bool GATED>
 __global__ void __launch_bounds__(256) gemv_kernel(Stage p) {

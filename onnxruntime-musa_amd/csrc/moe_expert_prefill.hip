@@ -1,38 +1,76 @@
 // moe_expert_prefill.hip -- grouped expert GEMM for large token counts
 // (prefill), bound by MFMA throughput.
 //
-// Each workgroup computes a 128 (rows of one expert) x 128 (weight rows) tile
-// with 4 wavefronts in a 2x2 arrangement, each wave 64x64 as 2x2
-// v_mfma_f32_32x32x16 tiles with fp32 accumulation.  K advances 64 at a time
-// through a double-buffered LDS stage: activations are copied as-is (fc1
-// gathers token rows through the dispatch permutation, so the permuted input
-// is never materialised), weights are dequantised in registers on the way
-// from HBM to LDS (scale folded into the 16-bit operand).
+// A workgroup computes a tile of 128 rows (tokens of one expert, dispatch
+// order) x 256 weight rows with 4 wavefronts; each wave owns 64 weight rows
+// (4 tiles of 16) for all 128 rows: 8 x 4 v_mfma_f32_16x16x32 tiles, fp32
+// accumulation in 128 registers.
 //
-// For gated activations the 128 weight rows of a tile are the gate rows and
-// the linear rows of the same 64 features, so a lane holds both halves of
-// each output and applies bias + activation in the epilogue.
-//
-// Tile order: the row tiles of one (expert, weight tile) are consecutive and
-// are mapped onto one XCD (hardware workgroup ids are dealt to the 8 XCDs
-// round-robin), so a weight tile is fetched from HBM once per XCD L2.
+//  * Weights never touch LDS.  Each lane streams 16-byte pieces of its weight
+//    row straight from HBM/L2 into registers with raw buffer loads, in the
+//    MFMA operand layout of the decode kernels: lane (col = lane%16,
+//    g = lane/16) covers k in [KG*g, KG*g + KG) of each stage and feeds 8 of
+//    them to each MFMA step.  Dequantisation (and a per-block scale) happens
+//    in registers right before the MFMA.  A register ring keeps the next
+//    stage's weights in flight.
+//  * Activations are the shared operand: one stage (128 rows x BK) is copied
+//    to LDS per workgroup (fc1 gathers token rows through the dispatch
+//    permutation, so the permuted input is never materialised), double
+//    buffered, one barrier per stage.  LDS traffic per MFMA is a quarter of a
+//    both-operands-in-LDS tile of the same size.
+//  * Gated activations: a wave's tiles 0,1 are the gate rows and tiles 2,3
+//    the linear rows of the same 32 features, so each lane holds both halves
+//    of its outputs and applies bias + activation in the epilogue.
+//  * Scales: per output channel -> epilogue (weights enter the MFMA as exact
+//    integers); per block -> folded into the 16-bit weights of each stage.
+//  * Tile order: groups of 8 weight tiles are swept across all row tiles of
+//    all experts, and each XCD (hardware workgroup ids are dealt to the 8
+//    XCDs round-robin) receives a contiguous range of that order, so the
+//    workgroups resident on one XCD share ~8 activation tiles and ~8 weight
+//    tiles in its L2.
+//  * fc2 may split K across workgroups; the partial sums land in separate
+//    fp32 planes of y2 that finalize adds in a fixed order.
 #include "moe_dequant.h"
 #include "moe_launch.h"
 
 namespace moe {
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64, LDK = BK + 8;
+constexpr int BM = 128;           // rows per workgroup tile
+constexpr int kMT = BM / 16;      // 16-row tiles per wave (every wave covers all rows)
+constexpr int kNT = 4;            // 16-wide weight tiles per wave
+constexpr int BN = 4 * kNT * 16;  // weight rows per workgroup tile
+constexpr int kGroupN = 8;        // weight tiles swept together over the row tiles
 constexpr int kXcds = 8;
 
-struct PrefillStage {
+enum PScale : int { kPsNone = 0, kPsChan = 1, kPsBlock = 2, kPsHalfBlock = 3 };
+
+template <int WF>
+struct PG {
+  static constexpr int BK = WF == kDense ? 64 : 128;  // k per stage
+  static constexpr int KG = BK / 4;                    // k per lane group per stage
+  static constexpr int NSTEP = KG / 8;                 // MFMA steps per stage
+  static constexpr int BVEC = WF == kInt4 ? 1 : 2;     // 16-byte weight loads per tile per stage
+  static constexpr int ROWB = BK * 2;                  // LDS bytes of one activation row per stage
+  static constexpr int ABUF = BM * ROWB;               // one staged activation stage
+  static constexpr int PIECES = ROWB / 16;             // 16-byte pieces per row per stage
+  static constexpr int RPI = 1024 / ROWB;              // rows per 1 KB LDS-load instruction
+  static constexpr int APW = BM / RPI / 4;             // LDS-load instructions per wave per stage
+  static constexpr int EBITS = WF == kInt4 ? 4 : (WF == kInt8 ? 8 : 16);
+  // XOR swizzle of a row's 16-byte pieces, so that the 16 rows one MFMA
+  // operand read touches fall into 16 different bank groups
+  static __device__ __forceinline__ int swz(int m) { return (m / (16 / PIECES)) % PIECES; }
+};
+
+struct PStage {
   const void* in;  // fc1: x [T, K]; fc2: act [rows, K]
+  int64_t in_rows;
   int64_t K, nfeat;
-  const uint8_t* w;  // gate / plain weights
+  const uint8_t* w;  // gate / plain weights [E, w_rows, K(/pack)]
   const void* s;
   const void* b;
   int64_t w_rows;
-  const uint8_t* wl;
+  const uint8_t* wl;  // linear weights (fc3 or the fused fc1)
   const void* sl;
   const void* bl;
   int64_t wl_rows;
@@ -43,16 +81,14 @@ struct PrefillStage {
   const int32_t* perm;
   const int32_t* tile_offsets;
   int64_t topk;
-  int32_t mslots;  // row-tile slots per weight tile (upper bound)
-  void* out;
+  int32_t mslots;   // row-tile slots (upper bound over all experts)
+  int32_t ntiles;   // weight tiles of BN rows (gated: BN/2 features)
+  int32_t ngroups;  // ceil(ntiles / kGroupN)
+  int32_t ksplit;   // K splits (partial planes of the output)
+  int32_t kstages;  // stages per K split
+  int64_t out_rows;
+  void* out;  // fc1: act [rows, nfeat] (AT); fc2: y2 [ksplit][rows, nfeat] fp32
 };
-
-template <int WF>
-constexpr int64_t row_bytes(int64_t K) {
-  return WF == kInt4 ? K / 2 : (WF == kInt8 ? K : 2 * K);
-}
-template <int WF>
-constexpr int kBVecs = WF == kInt4 ? 1 : (WF == kInt8 ? 2 : 4);  // 16-B loads per thread per K step
 
 __device__ __forceinline__ int remap_xcd(int b, int nb) {
   const int per = nb / kXcds, rem = nb % kXcds;
@@ -60,45 +96,25 @@ __device__ __forceinline__ int remap_xcd(int b, int nb) {
   return x < rem ? x * (per + 1) + local : rem * (per + 1) + (x - rem) * per + local;
 }
 
-// Scaled dequant of 8 weights held in `bits` (int4: 1 dword; int8: 2 dwords).
-template <typename AT, int WF>
-__device__ __forceinline__ u32x4_t dequant8(const u32x4_t* v, int d, float s, bool f16_scale,
-                                            half2_t s2) {
-  if constexpr (WF == kInt4) {
-    const uint32_t x = v[0][d];
-    if constexpr (sizeof(AT) > 0 && AT::kId == 10) {
-      if (f16_scale) {
-        u32x4_t r = dq4_f16_exact(x);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = h2_bits(bits_h2(r[i]) * s2);
-        return r;
-      }
-    }
-    return dq4_scaled<AT>(x, s);
-  } else {
-    const uint32_t x0 = v[d >> 1][(d & 1) * 2], x1 = v[d >> 1][(d & 1) * 2 + 1];
-    if constexpr (AT::kId == 10) {
-      if (f16_scale) {
-        u32x4_t r = dq8_f16_exact(x0, x1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = h2_bits(bits_h2(r[i]) * s2);
-        return r;
-      }
-    }
-    return dq8_scaled<AT>(x0, x1, s);
-  }
-}
+template <typename AT, int WF, int SM, typename ST, bool FC1, bool GATED>
+__global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
+  using G = PG<WF>;
+  constexpr int BK = G::BK, KG = G::KG, NSTEP = G::NSTEP, BVEC = G::BVEC;
+  // two stage buffers as separate objects, so the compiler can tell that the
+  // LDS loads filling one never alias the reads of the other
+  __shared__ __attribute__((aligned(1024))) uint8_t sA0[G::ABUF];
+  __shared__ __attribute__((aligned(1024))) uint8_t sA1[G::ABUF];
 
-template <typename AT, int WF, bool FC1>
-__global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(PrefillStage p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDK];
-
+  // ---- tile of this workgroup ----
   const int L = remap_xcd(blockIdx.x, gridDim.x);
-  const int ntile = L / p.mslots, mslot = L % p.mslots;
-  const int E = p.E;
-  if (mslot >= p.tile_offsets[E]) return;
-  int lo = 0, hi = E;  // last expert with tile_offsets[e] <= mslot
+  const int per_split = p.ngroups * p.mslots * kGroupN;
+  const int ks = L / per_split;
+  const int r0 = L % per_split;
+  const int nin = r0 % kGroupN;
+  const int mslot = (r0 / kGroupN) % p.mslots;
+  const int ntile = (r0 / kGroupN / p.mslots) * kGroupN + nin;
+  if (ntile >= p.ntiles || mslot >= p.tile_offsets[p.E]) return;
+  int lo = 0, hi = p.E;  // last expert with tile_offsets[e] <= mslot
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
     if (p.tile_offsets[mid] <= mslot) lo = mid;
@@ -108,224 +124,332 @@ __global__ void __launch_bounds__(256, 2) prefill_gemm_kernel(PrefillStage p) {
   const int row_begin = p.offsets[e] + (mslot - p.tile_offsets[e]) * BM;
   const int rows = min(BM, p.offsets[e + 1] - row_begin);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool gated = FC1 && p.gate_mode != kGateNone;
-  const int64_t K = p.K;
-  const int nk = static_cast<int>(K / BK);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-load bases are scalar
+  const int col = lane & 15, g = lane >> 4;
+  const int K = static_cast<int>(p.K);  // K < 2^31 (buffer offsets are 32-bit)
+  const int kbeg = ks * p.kstages * BK;
+  const int nst = min(p.kstages, (K - kbeg + BK - 1) / BK);
 
-  // ---- A loader: 4 rows x 16 B per thread per K step ----
-  const uint8_t* asrc[4];
-  const int acc16 = tid & 7;  // 16-byte column within the 128-byte row slice
+  // ---- weight rows of this wave's tiles: tile t of lane feature fl reads
+  // row row0 + drow[t] (gated: t < 2 gate, t >= 2 linear rows of the same
+  // features).  drow is uniform, so one VGPR offset per lane serves all tiles
+  // (the rest rides in the scalar offset).  Rows of features past nfeat are
+  // read (past the buffer: zeros) but their outputs are never stored. ----
+  const int64_t rb = static_cast<int64_t>(K) * G::EBITS / 8;  // bytes of one weight row
+  const uint8_t* wbase_g = p.w + static_cast<int64_t>(e) * p.w_rows * rb;
+  const uint8_t* wbase_l = p.wl + static_cast<int64_t>(e) * p.wl_rows * rb;
+  const __amdgpu_buffer_rsrc_t rs_g = make_rsrc(wbase_g, static_cast<uint32_t>(p.w_rows * rb));
+  const __amdgpu_buffer_rsrc_t rs_l = make_rsrc(wbase_l, static_cast<uint32_t>(p.wl_rows * rb));
+  const int64_t fbase = GATED ? static_cast<int64_t>(ntile) * (BN / 2) + wave * 32
+                              : static_cast<int64_t>(ntile) * BN + wave * 64;
+  const int64_t fl = fbase + col;
+  const bool interleaved = GATED && p.gate_mode == kGateInterleaved;
+  const int64_t row0 = interleaved ? 2 * fl : fl;
+  int64_t drow[kNT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (tid >> 3) + 32 * i;
-    asrc[i] = nullptr;
-    if (r < rows) {
-      const int64_t src = FC1 ? p.perm[row_begin + r] / p.topk : row_begin + r;
-      asrc[i] = static_cast<const uint8_t*>(p.in) + src * K * 2 + acc16 * 16;
-    }
-  }
-
-  // ---- B loader: one weight row, 32 k per thread per K step ----
-  const int brow = tid >> 1, bhalf = tid & 1;
-  int64_t feat, wrow;
-  const uint8_t* wbase;
-  const void* sbase;
-  int64_t srows;
-  if (gated) {
-    feat = static_cast<int64_t>(ntile) * (BN / 2) + (brow & 63);
-    const bool lin = brow >= 64;
-    if (p.gate_mode == kGateFc3) {
-      wrow = feat;
-      wbase = lin ? p.wl : p.w;
-      sbase = lin ? p.sl : p.s;
-      srows = lin ? p.wl_rows : p.w_rows;
+  for (int t = 0; t < kNT; ++t) {
+    if constexpr (GATED) {
+      const bool lin = t >= 2;
+      if (interleaved) drow[t] = 32 * (t & 1) + (lin ? 1 : 0);
+      else drow[t] = 16 * (t & 1) + ((lin && p.gate_mode == kGateChunked) ? p.nfeat : 0);
     } else {
-      wrow = p.gate_mode == kGateInterleaved ? 2 * feat + (lin ? 1 : 0) : feat + (lin ? p.nfeat : 0);
-      wbase = p.w;
-      sbase = p.s;
-      srows = p.w_rows;
+      drow[t] = 16 * t;
     }
-  } else {
-    feat = static_cast<int64_t>(ntile) * BN + brow;
-    wrow = feat;
-    wbase = p.w;
-    sbase = p.s;
-    srows = p.w_rows;
   }
-  const bool bok = feat < p.nfeat;
-  const int64_t rb = row_bytes<WF>(K);
-  const uint8_t* bsrc = wbase + (static_cast<int64_t>(e) * srows + (bok ? wrow : 0)) * rb;
-  const bool quant = WF != kDense;
-  const int64_t bs = p.block_size;
-  const int64_t nblk = quant ? (bs > 0 ? K / bs : 1) : 1;
-  const int64_t sidx = (static_cast<int64_t>(e) * srows + (bok ? wrow : 0)) * nblk;
-  const bool f16_scale = p.scale_type == MOE_ELEM_FLOAT16;
-  float chan_s = 1.0f;
-  if (quant && bs == 0 && bok) chan_s = load_any(sbase, p.scale_type, sidx);
+  const uint32_t woff = static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KG * g) * G::EBITS / 8);
 
-  constexpr int BV = kBVecs<WF>;
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-  u32x4_t ra[4], rbv[BV];
-
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      ra[i] = asrc[i] ? *reinterpret_cast<const u32x4_t*>(asrc[i] + static_cast<int64_t>(kt) * BK * 2) : z;
-    const int64_t boff = (static_cast<int64_t>(kt) * BK + 32 * bhalf) * rb / K;
-#pragma unroll
-    for (int v = 0; v < BV; ++v)
-      rbv[v] = bok ? *reinterpret_cast<const u32x4_t*>(bsrc + boff + 16 * v) : z;
+  // ---- per-block scales (folded): buffer loads of each tile row's scale of
+  // the lane's piece; pieces past K or of a padding stage read 0 ----
+  constexpr bool kFold = SM == kPsBlock || SM == kPsHalfBlock;
+  constexpr int SB = sizeof(typename ST::storage);
+  const int bshift = kFold ? __builtin_ctzll(static_cast<uint64_t>(p.block_size)) : 0;
+  const int64_t nblk = kFold ? (K >> bshift) : 0;
+  const __amdgpu_buffer_rsrc_t rs_sg =
+      make_rsrc(kFold ? static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk * SB : nullptr,
+                static_cast<uint32_t>(p.w_rows * nblk * SB));
+  const __amdgpu_buffer_rsrc_t rs_sl =
+      make_rsrc(kFold ? static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk * SB : nullptr,
+                static_cast<uint32_t>(p.wl_rows * nblk * SB));
+  const uint32_t soff = static_cast<uint32_t>(row0 * nblk * SB);
+  auto sload = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int64_t soffset) -> float {
+    if constexpr (SB == 4) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off),
+                                                                          static_cast<int>(soffset), 0));
+    } else {
+      const uint16_t h = __builtin_bit_cast(
+          uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), static_cast<int>(soffset), 0));
+      return to_f32<ST>(__builtin_bit_cast(typename ST::storage, h));
+    }
   };
-  auto sstore = [&](int kt, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (tid >> 3) + 32 * i;
-      *reinterpret_cast<u32x4_t*>(&sA[buf][r * LDK + acc16 * 8]) = ra[i];
+
+  struct Ring {
+    u32x4_t w[kNT][BVEC];
+    float sc[kNT][SM == kPsHalfBlock ? 2 : 1];
+  };
+  auto fetch = [&](int c, Ring& d) {
+    const int k0 = kbeg + c * BK + KG * g;  // first k of the lane's piece
+    const bool kin = (c < nst) & (k0 < K);
+    const uint32_t o = kin ? woff + static_cast<uint32_t>(c * BK * G::EBITS / 8) : kOob;
+    uint32_t so = kOob, so1 = kOob;
+    if constexpr (kFold) {
+      so = kin ? soff + static_cast<uint32_t>((k0 >> bshift) * SB) : kOob;
+      if constexpr (SM == kPsHalfBlock) so1 = kin ? soff + static_cast<uint32_t>(((k0 + 16) >> bshift) * SB) : kOob;
     }
-    uint16_t* dst = &sB[buf][brow * LDK + 32 * bhalf];
-    if constexpr (WF == kDense) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) *reinterpret_cast<u32x4_t*>(dst + 8 * v) = rbv[v];
-    } else {
+    for (int t = 0; t < kNT; ++t) {
+      const __amdgpu_buffer_rsrc_t rw = GATED && t >= 2 ? rs_l : rs_g;
+      const int sw = static_cast<int>(drow[t] * rb);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float s = chan_s;
-        if (bs > 0 && bok) s = load_any(sbase, p.scale_type, sidx + (static_cast<int64_t>(kt) * BK + 32 * bhalf + 8 * d) / bs);
-        const _Float16 sh = static_cast<_Float16>(s);
-        const half2_t s2 = {sh, sh};
-        *reinterpret_cast<u32x4_t*>(dst + 8 * d) = dequant8<AT, WF>(rbv, d, s, f16_scale, s2);
+      for (int v = 0; v < BVEC; ++v)
+        d.w[t][v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw, 0));
+      if constexpr (kFold) {
+        const __amdgpu_buffer_rsrc_t rs = GATED && t >= 2 ? rs_sl : rs_sg;
+        const int64_t ss = drow[t] * nblk * SB;
+        d.sc[t][0] = sload(rs, so, ss);
+        if constexpr (SM == kPsHalfBlock) d.sc[t][1] = sload(rs, so1, ss);
       }
     }
   };
 
-  // ---- MFMA tiles ----
-  const int wm = wave >> 1, wn = wave & 1;
-  // B-tile row bases of this wave's two 32-wide column blocks
-  int bcol[2];
-  if (gated) { bcol[0] = 32 * wn; bcol[1] = 64 + 32 * wn; }
-  else { bcol[0] = 64 * wn; bcol[1] = 64 * wn + 32; }
-  floatx16_t acc[2][2];
+  // ---- activation stages go global -> LDS directly (buffer loads with the
+  // LDS bit, 1 KB per wave instruction: lane L writes bytes [16 L, 16 L + 16)
+  // of the block).  Instruction j of wave w covers rows (w * APW + j) * RPI
+  // + L / PIECES; lane L's LDS piece p = L % PIECES holds the row's global
+  // piece p ^ swz(row).  Rows past the tile and k past K (or past the split)
+  // read zeros. ----
+  const __amdgpu_buffer_rsrc_t rs_x = make_rsrc(p.in, static_cast<uint32_t>(p.in_rows * K * 2));
+  auto apiece = [&](int j) {  // global piece of the lane in instruction j
+    const int r = (wave * G::APW + j) * G::RPI + lane / G::PIECES;
+    return (lane % G::PIECES) ^ G::swz(r);
+  };
+  uint32_t asrc[G::APW];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  const int lr = lane & 31, lk = (lane >> 5) * 8;
-  gload(0);
-  sstore(0, 0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      u32x4_t af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const u32x4_t*>(&sA[buf][(64 * wm + 32 * i + lr) * LDK + ks * 16 + lk]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const u32x4_t*>(&sB[buf][(bcol[j] + lr) * LDK + ks * 16 + lk]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16<AT>(af[i], bf[j], acc[i][j]);
+  for (int j = 0; j < G::APW; ++j) {
+    const int r = (wave * G::APW + j) * G::RPI + lane / G::PIECES;
+    if (r < rows) {
+      const int64_t src = FC1 ? p.perm[row_begin + r] / p.topk : row_begin + r;
+      asrc[j] = static_cast<uint32_t>((src * K + kbeg) * 2 + apiece(j) * 16);
+    } else {
+      asrc[j] = kOob;
     }
-    if (kt + 1 < nk) sstore(kt + 1, buf ^ 1);
+  }
+  auto aload = [&](int c, uint8_t* buf) {
+    const int krem = K - kbeg - c * BK;  // k left in the row from this stage on
+#pragma unroll
+    for (int j = 0; j < G::APW; ++j) {
+      const bool in = (c < nst) & (apiece(j) * 8 < krem);
+      const uint32_t o = in ? asrc[j] + static_cast<uint32_t>(c * BK * 2) : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs_x, (__attribute__((address_space(3))) void*)(buf + (wave * G::APW + j) * 1024), 16,
+          static_cast<int>(o), 0, 0, 0);
+    }
+  };
+
+  floatx4_t acc[kMT][kNT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i)
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) acc[i][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  // A operand of row tile i, step s: row m = 16 i + col, global piece
+  // gp0 + s; swz(m) does not depend on i
+  const int gp0 = KG * 2 * g / 16;
+  auto compute = [&](const uint8_t* buf, const Ring& d) {
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      const uint8_t* xa = buf + col * G::ROWB + ((gp0 + s) ^ G::swz(col)) * 16;
+      u32x4_t bw[kNT];
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) {
+        if constexpr (SM == kPsBlock && AT::kId == 10 && ST::kId == 10) {
+          // fp16: exact integers, then one packed multiply by the block scale
+          const u32x4_t q = weight_operand<AT, WF, false>(d.w[t], s, 0.0f);
+          const _Float16 sh = static_cast<_Float16>(d.sc[t][0]);
+          const half2_t s2 = {sh, sh};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bw[t][r] = h2_bits(bits_h2(q[r]) * s2);
+        } else if constexpr (kFold) {
+          const float sc = SM == kPsHalfBlock ? d.sc[t][s >> 1] : d.sc[t][0];
+          bw[t] = weight_operand<AT, WF, true>(d.w[t], s, sc);
+        } else {
+          bw[t] = weight_operand<AT, WF, false>(d.w[t], s, 0.0f);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + i * 16 * G::ROWB);
+#pragma unroll
+        for (int t = 0; t < kNT; ++t) acc[i][t] = mfma16x16x32<AT>(a, bw[t], acc[i][t]);
+      }
+      // keep each step's operands next to its MFMAs (bounds live registers)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- main loop: stages in pairs (buffers / ring slots 0 and 1).  Stage
+  // c + 1's activations and weights are requested before stage c is
+  // multiplied; the barrier after stage c waits for the LDS loads only (the
+  // weight loads issued after them stay in flight).  A padding stage past the
+  // split's range reads zeros. ----
+  Ring ring[2];
+  aload(0, sA0);
+  fetch(0, ring[0]);
+  __syncthreads();
+  const int npairs = (nst + 1) / 2;
+  for (int q = 0; q < npairs; ++q) {
+    const int c = 2 * q;
+    aload(c + 1, sA1);
+    fetch(c + 1, ring[1]);
+    compute(sA0, ring[0]);
+    __syncthreads();
+    aload(c + 2, sA0);
+    fetch(c + 2, ring[0]);
+    compute(sA1, ring[1]);
     __syncthreads();
   }
 
-  // ---- epilogue ----
-  // lane holds D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each 32x32 tile
+  // ---- epilogue: lane holds D[16 i + 4 g + r][col] of tile (i, t) ----
   const int act_t = AT::kId;
-  if (gated) {
-    const int64_t f = static_cast<int64_t>(ntile) * (BN / 2) + 32 * wn + lr;
-    if (f >= p.nfeat) return;
-    int64_t ng = f, nl = f;
-    if (p.gate_mode == kGateInterleaved) { ng = 2 * f; nl = 2 * f + 1; }
-    else if (p.gate_mode == kGateChunked) { nl = p.nfeat + f; }
-    float bg = 0.f, bl = 0.f;
-    if (p.b) bg = load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + ng);
-    if (p.bl) bl = load_any(p.bl, act_t, static_cast<int64_t>(e) * p.wl_rows + nl);
+  if constexpr (FC1 && GATED) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= rows) continue;
-        const float a = apply_act(acc[i][0][r] + bg, acc[i][1][r] + bl, true, p.activation,
-                                  p.alpha, p.beta, p.limit);
-        static_cast<typename AT::storage*>(p.out)[static_cast<int64_t>(row_begin + m) * p.nfeat + f] =
-            from_f32<AT>(a);
+    for (int t = 0; t < 2; ++t) {
+      const int64_t f = fl + t * 16;
+      if (f >= p.nfeat) continue;
+      const int64_t rg = row0 + drow[t], rl = row0 + drow[t + 2];
+      float chg = 1.0f, chl = 1.0f;
+      if constexpr (SM == kPsChan) {
+        chg = load_any(p.s, p.scale_type, static_cast<int64_t>(e) * p.w_rows + rg);
+        chl = load_any(p.sl, p.scale_type, static_cast<int64_t>(e) * p.wl_rows + rl);
       }
+      const float bg = p.b ? load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + rg) : 0.0f;
+      const float bl = p.bl ? load_any(p.bl, act_t, static_cast<int64_t>(e) * p.wl_rows + rl) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * i + 4 * g + r;
+          if (m >= rows) continue;
+          const float a = apply_act(acc[i][t][r] * chg + bg, acc[i][t + 2][r] * chl + bl, true, p.activation,
+                                    p.alpha, p.beta, p.limit);
+          static_cast<typename AT::storage*>(p.out)[static_cast<int64_t>(row_begin + m) * p.nfeat + f] =
+              from_f32<AT>(a);
+        }
+    }
   } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t f = static_cast<int64_t>(ntile) * BN + bcol[j] + lr;
+    for (int t = 0; t < kNT; ++t) {
+      const int64_t f = fl + t * 16;
       if (f >= p.nfeat) continue;
-      float bias = 0.f;
-      if (p.b) bias = load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + f);
+      float ch = 1.0f;
+      if constexpr (SM == kPsChan) ch = load_any(p.s, p.scale_type, static_cast<int64_t>(e) * p.w_rows + f);
+      const float bias = (p.b && ks == 0) ? load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + f) : 0.0f;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kMT; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * i + 4 * g + r;
           if (m >= rows) continue;
-          const float v = acc[i][j][r] + bias;
+          const float v = acc[i][t][r] * ch + bias;
           const int64_t o = static_cast<int64_t>(row_begin + m) * p.nfeat + f;
           if constexpr (FC1) {
             static_cast<typename AT::storage*>(p.out)[o] = from_f32<AT>(act_single(v, p.activation));
           } else {
-            static_cast<float*>(p.out)[o] = v;
+            static_cast<float*>(p.out)[static_cast<int64_t>(ks) * p.out_rows * p.nfeat + o] = v;
           }
         }
     }
   }
 }
 
-template <typename AT, int WF, bool FC1>
-hipError_t launch_typed(const PrefillStage& st, int64_t ntiles, hipStream_t stream) {
-  const int64_t nb = ntiles * st.mslots;
-  hipLaunchKernelGGL((prefill_gemm_kernel<AT, WF, FC1>), dim3(static_cast<unsigned>(nb)), dim3(256), 0,
-                     stream, st);
+template <typename AT, int WF, int SM, typename ST, bool FC1>
+hipError_t launch_kernel(const PStage& st, bool gated, hipStream_t stream) {
+  const unsigned nb = static_cast<unsigned>(st.ksplit) * st.ngroups * st.mslots * kGroupN;
+  if (FC1 && gated)
+    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, true, true>), dim3(nb), dim3(256), 0, stream, st);
+  else
+    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, FC1, false>), dim3(nb), dim3(256), 0, stream, st);
   return hipGetLastError();
 }
 
-template <bool FC1>
-hipError_t launch_stage(const PrefillStage& st, const ExpertArgs& a, int64_t ntiles, hipStream_t stream) {
-  const bool bf = a.act_type == MOE_ELEM_BFLOAT16;
-  switch (a.wfmt) {
-    case kInt4: return bf ? launch_typed<BF16, kInt4, FC1>(st, ntiles, stream)
-                          : launch_typed<F16, kInt4, FC1>(st, ntiles, stream);
-    case kInt8: return bf ? launch_typed<BF16, kInt8, FC1>(st, ntiles, stream)
-                          : launch_typed<F16, kInt8, FC1>(st, ntiles, stream);
-    default: return bf ? launch_typed<BF16, kDense, FC1>(st, ntiles, stream)
-                       : launch_typed<F16, kDense, FC1>(st, ntiles, stream);
+template <typename AT, int WF, bool FC1>
+hipError_t launch_scaled(const PStage& st, const ExpertArgs& a, bool gated, hipStream_t stream) {
+  if constexpr (WF == kDense) {
+    return launch_kernel<AT, WF, kPsNone, F16, FC1>(st, gated, stream);
+  } else {
+    if (a.block_size == 0) return launch_kernel<AT, WF, kPsChan, F16, FC1>(st, gated, stream);
+    const bool half = a.block_size < PG<WF>::KG;  // 16: two blocks per lane piece
+    auto by_type = [&](auto st_tag) -> hipError_t {
+      using ST = decltype(st_tag);
+      return half ? launch_kernel<AT, WF, kPsHalfBlock, ST, FC1>(st, gated, stream)
+                  : launch_kernel<AT, WF, kPsBlock, ST, FC1>(st, gated, stream);
+    };
+    if (a.scale_type == MOE_ELEM_FLOAT) return by_type(F32{});
+    if (a.scale_type == MOE_ELEM_BFLOAT16) return by_type(BF16{});
+    return by_type(F16{});
   }
 }
 
-int32_t mslots_for(const ExpertArgs& a) {
-  return static_cast<int32_t>((a.T * a.k + BM - 1) / BM + a.E);
+template <bool FC1>
+hipError_t launch_stage(const PStage& st, const ExpertArgs& a, bool gated, hipStream_t stream) {
+  const bool bf = a.act_type == MOE_ELEM_BFLOAT16;
+  switch (a.wfmt) {
+    case kInt4: return bf ? launch_scaled<BF16, kInt4, FC1>(st, a, gated, stream)
+                          : launch_scaled<F16, kInt4, FC1>(st, a, gated, stream);
+    case kInt8: return bf ? launch_scaled<BF16, kInt8, FC1>(st, a, gated, stream)
+                          : launch_scaled<F16, kInt8, FC1>(st, a, gated, stream);
+    default: return bf ? launch_scaled<BF16, kDense, FC1>(st, a, gated, stream)
+                       : launch_scaled<F16, kDense, FC1>(st, a, gated, stream);
+  }
+}
+
+int32_t mslots_for(int64_t T, int64_t k, int64_t E) {
+  return static_cast<int32_t>((T * k + BM - 1) / BM + E);
+}
+
+int bk_for(int wfmt) { return wfmt == kDense ? PG<kDense>::BK : PG<kInt4>::BK; }
+
+void plan_grid(PStage& st, int64_t T, int64_t k, int64_t E, int wfmt, int64_t nrows_w, int32_t ksplit) {
+  st.mslots = mslots_for(T, k, E);
+  st.ntiles = static_cast<int32_t>((nrows_w + BN - 1) / BN);
+  st.ngroups = (st.ntiles + kGroupN - 1) / kGroupN;
+  const int64_t bk = bk_for(wfmt);
+  const int64_t stages = (st.K + bk - 1) / bk;
+  st.ksplit = ksplit;
+  st.kstages = static_cast<int32_t>((stages + ksplit - 1) / ksplit);
 }
 
 }  // namespace
 
+int32_t prefill_fc2_splits(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt) {
+  // Split K in two when the fc2 tiles would leave a partial last wave of
+  // workgroups over the 256 CUs (2 resident per CU) and K is long enough.
+  const int64_t tiles = ((T * k + BM - 1) / BM + std::min<int64_t>(E, T * k)) * ((H + BN - 1) / BN);
+  const int64_t stages = (I + bk_for(wfmt) - 1) / bk_for(wfmt);
+  return (tiles < 2048 && stages >= 32) ? 2 : 1;
+}
+
 bool prefill_supported(const ExpertArgs& a) {
   if (a.act_type != MOE_ELEM_FLOAT16 && a.act_type != MOE_ELEM_BFLOAT16) return false;
-  if (a.H % BK || a.I % BK) return false;
-  if (a.wfmt != kDense && a.block_size > 0 && a.block_size < 8) return false;
+  if (a.H % 32 || a.I % 32) return false;
+  if (a.wfmt != kDense && a.block_size > 0 && a.block_size < 16) return false;
+  // 32-bit buffer offsets: one expert's weights and the activation rows stay below 2 GiB
+  const int64_t lim = int64_t{1} << 31;
+  const int64_t ebits = a.wfmt == kInt4 ? 4 : (a.wfmt == kInt8 ? 8 : 16);
+  const int64_t n1 = (a.gate_mode == kGateInterleaved || a.gate_mode == kGateChunked) ? 2 * a.I : a.I;
+  if (n1 * a.H * ebits / 8 >= lim || a.H * a.I * ebits / 8 >= lim) return false;
+  if (a.T * a.k * std::max(a.H, a.I) * 2 >= lim) return false;
   return true;
 }
 
 hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream) {
-  PrefillStage st{};
+  PStage st{};
   st.in = a.x;
+  st.in_rows = a.T;
   st.K = a.H;
   st.nfeat = a.I;
   const bool fused = a.gate_mode == kGateInterleaved || a.gate_mode == kGateChunked;
+  const bool gated = a.gate_mode != kGateNone;
   st.w = static_cast<const uint8_t*>(a.w1);
   st.s = a.s1;
   st.b = a.b1;
@@ -353,15 +477,17 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream) {
   st.perm = a.perm;
   st.tile_offsets = a.tile_offsets;
   st.topk = a.k;
-  st.mslots = mslots_for(a);
+  st.out_rows = a.T * a.k;
   st.out = a.act;
-  const int64_t per_tile = a.gate_mode != kGateNone ? BN / 2 : BN;
-  return launch_stage<true>(st, a, (a.I + per_tile - 1) / per_tile, stream);
+  // gated: a weight tile holds BN/2 features (gate + linear rows)
+  plan_grid(st, a.T, a.k, a.E, a.wfmt, gated ? 2 * a.I : a.I, 1);
+  return launch_stage<true>(st, a, gated, stream);
 }
 
-hipError_t launch_fc2_prefill(const ExpertArgs& a, hipStream_t stream) {
-  PrefillStage st{};
+hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, hipStream_t stream) {
+  PStage st{};
   st.in = a.act;
+  st.in_rows = a.T * a.k;
   st.K = a.I;
   st.nfeat = a.H;
   st.w = static_cast<const uint8_t*>(a.w2);
@@ -381,9 +507,12 @@ hipError_t launch_fc2_prefill(const ExpertArgs& a, hipStream_t stream) {
   st.perm = a.perm;
   st.tile_offsets = a.tile_offsets;
   st.topk = a.k;
-  st.mslots = mslots_for(a);
+  st.out_rows = a.T * a.k;
   st.out = a.y2;
-  return launch_stage<false>(st, a, (a.H + BN - 1) / BN, stream);
+  const int32_t splits = prefill_fc2_splits(a.T, a.H, a.I, a.E, a.k, a.wfmt);
+  plan_grid(st, a.T, a.k, a.E, a.wfmt, a.H, splits);
+  *y2_planes = splits;
+  return launch_stage<false>(st, a, false, stream);
 }
 
 }  // namespace moe

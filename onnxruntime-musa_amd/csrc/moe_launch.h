@@ -34,8 +34,6 @@ struct RouteArgs {
   moe_route_params p;
   int32_t* tile_offsets;  // optional [E+1]: prefix of ceil(count_e / tile_m)
   int32_t tile_m;
-  int32_t* zero;          // optional: counters cleared to 0 by the routing kernel
-  int64_t zero_count;
 };
 
 size_t route_scratch_bytes(int64_t T, int64_t E, int64_t k);
@@ -67,8 +65,6 @@ struct ExpertArgs {
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
   int32_t y2_planes;
-  float* fc1_part;        // decode fc1 partial planes (K split across workgroups)
-  int32_t* fc1_arrive;    // decode fc1 per-tile arrival counters (zeroed by routing)
   void* out;   // [T, H] act_type
 };
 
@@ -77,13 +73,15 @@ hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
 hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
-hipError_t launch_fc2_prefill(const ExpertArgs& a, hipStream_t stream);
+hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
 
 // Whether the MFMA paths accept this problem (fp16/bf16 activations, K a
 // multiple of 32, block sizes the dequant loaders handle).
 bool decode_supported(const ExpertArgs& a);
 bool prefill_supported(const ExpertArgs& a);
+// K splits (partial planes of y2) the prefill fc2 kernel uses for a problem.
+int32_t prefill_fc2_splits(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt);
 
 // Row tile of the prefill grouped GEMM (rows of one expert per workgroup).
 constexpr int kPrefillTileM = 128;
@@ -101,8 +99,6 @@ struct DecodePlan {
   bool lds2 = false;        // fc2: activation slice staged in LDS
   int32_t ksg1 = 1, kr1 = 0, fgroups1 = 0;  // fc1 K groups, K per group, feature groups
   int32_t ksg2 = 1, kr2 = 0;                // fc2 K groups, K per group
-  int64_t fc1_part_floats = 0;              // partial-plane storage of fc1
-  int64_t arrive_count = 0;                 // arrival counters of fc1
   int32_t y2_planes_max = 1;
 };
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode);

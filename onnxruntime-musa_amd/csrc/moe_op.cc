@@ -66,7 +66,8 @@ struct Problem {
 
 // Workspace sections, byte offsets from the workspace base.
 struct Layout {
-  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, fc1_part, arrive, total;
+  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, total;
+  int32_t y2_planes;
   size_t route_scratch_bytes;
   moe::DecodePlan decode;
 };
@@ -90,10 +91,9 @@ Layout plan_layout(const Problem& p) {
   l.route_scratch = take(l.route_scratch_bytes);
   l.act = take(rows * static_cast<size_t>(p.I) * elem_size(p.act_type));
   l.decode = moe::plan_decode(p.T, p.H, p.I, p.E, p.k, p.wfmt, p.gate_mode);
-  const size_t planes = static_cast<size_t>(std::max<int32_t>(1, l.decode.y2_planes_max));
-  l.y2 = take(rows * static_cast<size_t>(p.H) * 4 * planes);
-  l.fc1_part = take(static_cast<size_t>(l.decode.fc1_part_floats) * 4);
-  l.arrive = take(static_cast<size_t>(l.decode.arrive_count) * 4);
+  l.y2_planes = std::max<int32_t>({1, l.decode.y2_planes_max,
+                                    moe::prefill_fc2_splits(p.T, p.H, p.I, p.E, p.k, p.wfmt)});
+  l.y2 = take(rows * static_cast<size_t>(p.H) * 4 * static_cast<size_t>(l.y2_planes));
   l.total = o;
   return l;
 }
@@ -292,8 +292,6 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
   a.y2_planes = 1;
-  a.fc1_part = reinterpret_cast<float*>(ws + l.fc1_part);
-  a.fc1_arrive = reinterpret_cast<int32_t*>(ws + l.arrive);
   a.out = output;
   return a;
 }
@@ -418,7 +416,7 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
     out->total = l.total;
     out->act = l.act;
     out->y2 = l.y2;
-    out->y2_planes_max = static_cast<size_t>(std::max<int32_t>(l.decode.y2_planes_max, 1));
+    out->y2_planes_max = static_cast<size_t>(l.y2_planes);
     return MOE_OK;
   } catch (const std::exception& e) {
     return fail(MOE_FAIL, e.what());
@@ -480,8 +478,6 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     ra.p.scratch_bytes = l.route_scratch_bytes;
     ra.tile_offsets = reinterpret_cast<int32_t*>(ws + l.tile_offsets);
     ra.tile_m = moe::kPrefillTileM;
-    ra.zero = reinterpret_cast<int32_t*>(ws + l.arrive);
-    ra.zero_count = l.decode.arrive_count;
     moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
     const int path = choose_path(kernel, a);
     if (path < 0) return fail(MOE_NOT_IMPLEMENTED, "forced expert path does not support this problem");
@@ -505,7 +501,7 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
       case moe::kPathPrefill:
         e = moe::launch_fc1_prefill(a, stream);
         mark(2);
-        if (e == hipSuccess) e = moe::launch_fc2_prefill(a, stream);
+        if (e == hipSuccess) e = moe::launch_fc2_prefill(a, &a.y2_planes, stream);
         break;
       default:
         e = moe::launch_fc1_simt(a, stream);

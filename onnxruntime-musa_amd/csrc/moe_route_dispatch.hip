@@ -213,7 +213,6 @@ __global__ void __launch_bounds__(1024) route_dispatch_small_kernel(RouteArgs a)
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int nwaves = blockDim.x / kWave;
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
-  for (int64_t i = tid; i < a.zero_count; i += blockDim.x) a.zero[i] = 0;
   __syncthreads();
   for (int64_t t = wave; t < T; t += nwaves) {
     int id;
@@ -267,7 +266,6 @@ __global__ void __launch_bounds__(1024) dispatch_scan_kernel(RouteArgs a, int32_
   __shared__ int cnt[kMaxExperts];
   __shared__ int base[kMaxExperts];
   const int E = static_cast<int>(a.p.num_experts);
-  for (int64_t i = threadIdx.x; i < a.zero_count; i += blockDim.x) a.zero[i] = 0;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int run = 0;
     for (int b = 0; b < nblocks; ++b) {
