@@ -25,16 +25,22 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t h2_bits(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
 __device__ __forceinline__ half2_t bits_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
 
-// int4 dword (k0..k7) -> fp16 pairs of (nibble - 8), exact.
+// int4 dword (k0..k7) -> fp16 pairs of (nibble - 8), exact.  The nibble
+// bytes are first put in k order (one permute per 4 k), then each output
+// dword takes two of them under 0x64 high bytes (the magic 1024 + q) with a
+// second permute against a constant, and one packed subtract removes 1032.
 __device__ __forceinline__ u32x4_t dq4_f16_exact(uint32_t v) {
-  const uint32_t t = v & 0x0F0F0F0Fu;         // even k nibbles, one per byte
-  const uint32_t u = (v >> 4) & 0x0F0F0F0Fu;  // odd k nibbles
+  const uint32_t x = v & 0x0F0F0F0Fu;         // k0, k2, k4, k6
+  const uint32_t y = (v >> 4) & 0x0F0F0F0Fu;  // k1, k3, k5, k7
+  const uint32_t z0 = __builtin_amdgcn_perm(y, x, 0x05010400u);  // bytes k0 k1 k2 k3
+  const uint32_t z1 = __builtin_amdgcn_perm(y, x, 0x07030602u);  // bytes k4 k5 k6 k7
+  const uint32_t c = 0x64646464u;
   const half2_t bias = {static_cast<_Float16>(1032.0f), static_cast<_Float16>(1032.0f)};
   u32x4_t r;
-  r[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c040c00u) | 0x64006400u) - bias);
-  r[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c050c01u) | 0x64006400u) - bias);
-  r[2] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c060c02u) | 0x64006400u) - bias);
-  r[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(u, t, 0x0c070c03u) | 0x64006400u) - bias);
+  r[0] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, z0, 0x04010400u)) - bias);
+  r[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, z0, 0x04030402u)) - bias);
+  r[2] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, z1, 0x04010400u)) - bias);
+  r[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(c, z1, 0x04030402u)) - bias);
   return r;
 }
 

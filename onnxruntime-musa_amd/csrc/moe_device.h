@@ -76,32 +76,46 @@ enum Act : int { kRelu = 0, kGelu = 1, kSilu = 2, kIdentity = 3, kSwiglu = 4 };
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// FAST: sigmoid from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32;
+// about 1 ulp each, far below the 16-bit output rounding of the MFMA paths).
+// Saturates correctly: exp2 overflows to +inf -> 0, underflows to 0 -> 1.
+template <bool FAST>
+__device__ __forceinline__ float sigmoid_t(float x) {
+  if constexpr (FAST) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+  } else {
+    return sigmoid_f(x);
+  }
+}
+
+template <bool FAST = false>
 __device__ __forceinline__ float act_single(float x, int act) {
   switch (act) {
     case kRelu: return x > 0.0f ? x : 0.0f;
     case kGelu: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
-    case kSilu: return x * sigmoid_f(x);
+    case kSilu: return x * sigmoid_t<FAST>(x);
     default: return x;
   }
 }
 
 // SwiGLU with clamp: G = min(g, limit), L = clamp(l, -limit, limit),
 // out = G * sigmoid(alpha * G) * (L + beta).
-__device__ __forceinline__ float swiglu_f(float g, float l, float alpha, float beta,
-                                          float limit) {
+template <bool FAST = false>
+__device__ __forceinline__ float swiglu_f(float g, float l, float alpha, float beta, float limit) {
   g = fminf(g, limit);
   l = fminf(fmaxf(l, -limit), limit);
-  return g * sigmoid_f(alpha * g) * (l + beta);
+  return g * sigmoid_t<FAST>(alpha * g) * (l + beta);
 }
 
 // Combines a gate value and (if gated) a linear value into one activation.
 // gated == false: act(g).  activation == swiglu: swiglu(g, l).  Otherwise
-// act(g) * l (fc3 gating).
-__device__ __forceinline__ float apply_act(float g, float l, bool gated, int act, float alpha,
-                                           float beta, float limit) {
-  if (!gated) return act_single(g, act);
-  if (act == kSwiglu) return swiglu_f(g, l, alpha, beta, limit);
-  return act_single(g, act) * l;
+// act(g) * l (fc3 gating).  FAST selects the hardware sigmoid (16-bit outputs).
+template <bool FAST = false>
+__device__ __forceinline__ float apply_act(float g, float l, bool gated, int act, float alpha, float beta,
+                                           float limit) {
+  if (!gated) return act_single<FAST>(g, act);
+  if (act == kSwiglu) return swiglu_f<FAST>(g, l, alpha, beta, limit);
+  return act_single<FAST>(g, act) * l;
 }
 
 }  // namespace moe

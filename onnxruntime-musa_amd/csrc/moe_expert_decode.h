@@ -309,7 +309,7 @@ __global__ void __launch_bounds__(256) gemv_kernel(Stage p) {
         const int64_t o = static_cast<int64_t>(row0 + m) * p.nfeat + f;
         if constexpr (FC1) {
           const float vl = GATED ? acc[tl][q][r] * chl + bl : 0.0f;
-          const float a = apply_act(vg, vl, GATED, p.activation, p.alpha, p.beta, p.limit);
+          const float a = apply_act<true>(vg, vl, GATED, p.activation, p.alpha, p.beta, p.limit);
           static_cast<typename AT::storage*>(p.out)[o] = from_f32<AT>(a);
         } else {
           static_cast<float*>(p.out)[static_cast<int64_t>(blockIdx.z) * p.out_rows * p.nfeat + o] = vg;

@@ -260,7 +260,7 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
       }
       const float bg = p.b ? load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + trow[tg]) : 0.0f;
       const float bl = (GATED && p.bl) ? load_any(p.bl, act_t, static_cast<int64_t>(e) * p.wl_rows + trow[tl]) : 0.0f;
-      const float a = apply_act(vg * chg + bg, vl * chl + bl, GATED, p.activation, p.alpha, p.beta, p.limit);
+      const float a = apply_act<true>(vg * chg + bg, vl * chl + bl, GATED, p.activation, p.alpha, p.beta, p.limit);
       const int64_t f = fbase + ft * 16 + col;
       static_cast<typename AT::storage*>(p.out)[static_cast<int64_t>(row0 + m) * p.nfeat + f] = from_f32<AT>(a);
     };

@@ -30,6 +30,8 @@
 //    tiles in its L2.
 //  * fc2 may split K across workgroups; the partial sums land in separate
 //    fp32 planes of y2 that finalize adds in a fixed order.
+#include <algorithm>
+
 #include "moe_dequant.h"
 #include "moe_launch.h"
 
@@ -37,28 +39,28 @@ namespace moe {
 namespace {
 
 constexpr int BM = 128;           // rows per workgroup tile
-constexpr int kMT = BM / 16;      // 16-row tiles per wave (every wave covers all rows)
-constexpr int kNT = 4;            // 16-wide weight tiles per wave
-constexpr int BN = 4 * kNT * 16;  // weight rows per workgroup tile
+constexpr int kMT = BM / 32;      // 32-row blocks per wave (every wave covers all rows)
+constexpr int kNT = 2;            // 32-wide weight blocks per wave
+constexpr int BN = 4 * kNT * 32;  // weight rows per workgroup tile
 constexpr int kGroupN = 8;        // weight tiles swept together over the row tiles
 constexpr int kXcds = 8;
 
-enum PScale : int { kPsNone = 0, kPsChan = 1, kPsBlock = 2, kPsHalfBlock = 3 };
+enum PScale : int { kPsNone = 0, kPsChan = 1, kPsBlock = 2 };
 
 template <int WF>
 struct PG {
   static constexpr int BK = WF == kDense ? 64 : 128;  // k per stage
-  static constexpr int KG = BK / 4;                    // k per lane group per stage
-  static constexpr int NSTEP = KG / 8;                 // MFMA steps per stage
-  static constexpr int BVEC = WF == kInt4 ? 1 : 2;     // 16-byte weight loads per tile per stage
+  static constexpr int KH = BK / 2;                    // k per lane half per stage
+  static constexpr int NSTEP = KH / 8;                 // MFMA steps per stage
+  static constexpr int EBITS = WF == kInt4 ? 4 : (WF == kInt8 ? 8 : 16);
+  static constexpr int BVEC = KH * EBITS / 8 / 16;     // 16-byte weight loads per block per stage
   static constexpr int ROWB = BK * 2;                  // LDS bytes of one activation row per stage
   static constexpr int ABUF = BM * ROWB;               // one staged activation stage
   static constexpr int PIECES = ROWB / 16;             // 16-byte pieces per row per stage
   static constexpr int RPI = 1024 / ROWB;              // rows per 1 KB LDS-load instruction
   static constexpr int APW = BM / RPI / 4;             // LDS-load instructions per wave per stage
-  static constexpr int EBITS = WF == kInt4 ? 4 : (WF == kInt8 ? 8 : 16);
-  // XOR swizzle of a row's 16-byte pieces, so that the 16 rows one MFMA
-  // operand read touches fall into 16 different bank groups
+  // XOR swizzle of a row's 16-byte pieces: the 8 rows one 128-byte LDS
+  // cycle of an operand read touches fall into different bank groups
   static __device__ __forceinline__ int swz(int m) { return (m / (16 / PIECES)) % PIECES; }
 };
 
@@ -96,10 +98,18 @@ __device__ __forceinline__ int remap_xcd(int b, int nb) {
   return x < rem ? x * (per + 1) + local : rem * (per + 1) + (x - rem) * per + local;
 }
 
-template <typename AT, int WF, int SM, typename ST, bool FC1, bool GATED>
+// MFMA layout (v_mfma_f32_32x32x16): lane l = 32 h + r holds A row r / B
+// column r for k group h (8 k); D element (row 8 (q / 4) + 4 h + q % 4,
+// column r) in accumulator register q.  Within a stage, lane half h covers
+// k in [KH h, KH h + KH) and feeds k = KH h + 8 s .. + 7 to MFMA step s; the
+// activation operand is read with the same assignment.
+//
+// NSC: block scales per lane half and stage (KH / block_size, at least 1).
+template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATED>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   using G = PG<WF>;
-  constexpr int BK = G::BK, KG = G::KG, NSTEP = G::NSTEP, BVEC = G::BVEC;
+  constexpr int BK = G::BK, KH = G::KH, NSTEP = G::NSTEP, BVEC = G::BVEC;
+  constexpr bool kFold = SM == kPsBlock;
   // two stage buffers as separate objects, so the compiler can tell that the
   // LDS loads filling one never alias the reads of the other
   __shared__ __attribute__((aligned(1024))) uint8_t sA0[G::ABUF];
@@ -126,42 +136,37 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-load bases are scalar
-  const int col = lane & 15, g = lane >> 4;
+  const int lr = lane & 31, h = lane >> 5;
   const int K = static_cast<int>(p.K);  // K < 2^31 (buffer offsets are 32-bit)
   const int kbeg = ks * p.kstages * BK;
   const int nst = min(p.kstages, (K - kbeg + BK - 1) / BK);
 
-  // ---- weight rows of this wave's tiles: tile t of lane feature fl reads
-  // row row0 + drow[t] (gated: t < 2 gate, t >= 2 linear rows of the same
-  // features).  drow is uniform, so one VGPR offset per lane serves all tiles
-  // (the rest rides in the scalar offset).  Rows of features past nfeat are
-  // read (past the buffer: zeros) but their outputs are never stored. ----
+  // ---- weight rows: block j of lane feature fl reads row row0 + drow[j]
+  // (gated: j = 0 gate, j = 1 linear row of the same feature).  drow is
+  // uniform, so one VGPR offset per lane serves both blocks (the rest rides in
+  // the scalar offset).  Rows of features past nfeat are read (past the
+  // buffer: zeros) but their outputs are never stored. ----
   const int64_t rb = static_cast<int64_t>(K) * G::EBITS / 8;  // bytes of one weight row
   const uint8_t* wbase_g = p.w + static_cast<int64_t>(e) * p.w_rows * rb;
   const uint8_t* wbase_l = p.wl + static_cast<int64_t>(e) * p.wl_rows * rb;
   const __amdgpu_buffer_rsrc_t rs_g = make_rsrc(wbase_g, static_cast<uint32_t>(p.w_rows * rb));
   const __amdgpu_buffer_rsrc_t rs_l = make_rsrc(wbase_l, static_cast<uint32_t>(p.wl_rows * rb));
-  const int64_t fbase = GATED ? static_cast<int64_t>(ntile) * (BN / 2) + wave * 32
-                              : static_cast<int64_t>(ntile) * BN + wave * 64;
-  const int64_t fl = fbase + col;
+  const int64_t fl = GATED ? static_cast<int64_t>(ntile) * (BN / 2) + wave * 32 + lr
+                           : static_cast<int64_t>(ntile) * BN + wave * 64 + lr;
   const bool interleaved = GATED && p.gate_mode == kGateInterleaved;
   const int64_t row0 = interleaved ? 2 * fl : fl;
   int64_t drow[kNT];
-#pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    if constexpr (GATED) {
-      const bool lin = t >= 2;
-      if (interleaved) drow[t] = 32 * (t & 1) + (lin ? 1 : 0);
-      else drow[t] = 16 * (t & 1) + ((lin && p.gate_mode == kGateChunked) ? p.nfeat : 0);
-    } else {
-      drow[t] = 16 * t;
-    }
+  if constexpr (GATED) {
+    drow[0] = 0;
+    drow[1] = interleaved ? 1 : (p.gate_mode == kGateChunked ? p.nfeat : 0);
+  } else {
+    drow[0] = 0;
+    drow[1] = 32;
   }
-  const uint32_t woff = static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KG * g) * G::EBITS / 8);
+  const uint32_t woff = static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
 
-  // ---- per-block scales (folded): buffer loads of each tile row's scale of
-  // the lane's piece; pieces past K or of a padding stage read 0 ----
-  constexpr bool kFold = SM == kPsBlock || SM == kPsHalfBlock;
+  // ---- per-block scales (folded): buffer loads of each block row's scales
+  // for the lane's k range; ranges past K or of a padding stage read 0 ----
   constexpr int SB = sizeof(typename ST::storage);
   const int bshift = kFold ? __builtin_ctzll(static_cast<uint64_t>(p.block_size)) : 0;
   const int64_t nblk = kFold ? (K >> bshift) : 0;
@@ -177,39 +182,60 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off),
                                                                           static_cast<int>(soffset), 0));
     } else {
-      const uint16_t h = __builtin_bit_cast(
+      const uint16_t v = __builtin_bit_cast(
           uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), static_cast<int>(soffset), 0));
-      return to_f32<ST>(__builtin_bit_cast(typename ST::storage, h));
+      return to_f32<ST>(__builtin_bit_cast(typename ST::storage, v));
     }
   };
 
   struct Ring {
     u32x4_t w[kNT][BVEC];
-    float sc[kNT][SM == kPsHalfBlock ? 2 : 1];
+    float sc[kNT][kFold ? NSC : 1];
   };
   auto fetch = [&](int c, Ring& d) {
-    const int k0 = kbeg + c * BK + KG * g;  // first k of the lane's piece
+    const int k0 = kbeg + c * BK + KH * h;  // first k of the lane's range
     const bool kin = (c < nst) & (k0 < K);
     const uint32_t o = kin ? woff + static_cast<uint32_t>(c * BK * G::EBITS / 8) : kOob;
-    uint32_t so = kOob, so1 = kOob;
-    if constexpr (kFold) {
-      so = kin ? soff + static_cast<uint32_t>((k0 >> bshift) * SB) : kOob;
-      if constexpr (SM == kPsHalfBlock) so1 = kin ? soff + static_cast<uint32_t>(((k0 + 16) >> bshift) * SB) : kOob;
-    }
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const __amdgpu_buffer_rsrc_t rw = GATED && t >= 2 ? rs_l : rs_g;
-      const int sw = static_cast<int>(drow[t] * rb);
+    for (int j = 0; j < kNT; ++j) {
+      const __amdgpu_buffer_rsrc_t rw = GATED && j == 1 ? rs_l : rs_g;
+      const int sw = static_cast<int>(drow[j] * rb);
 #pragma unroll
       for (int v = 0; v < BVEC; ++v)
-        d.w[t][v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw, 0));
+        d.w[j][v] = __builtin_bit_cast(
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw, 0));
       if constexpr (kFold) {
-        const __amdgpu_buffer_rsrc_t rs = GATED && t >= 2 ? rs_sl : rs_sg;
-        const int64_t ss = drow[t] * nblk * SB;
-        d.sc[t][0] = sload(rs, so, ss);
-        if constexpr (SM == kPsHalfBlock) d.sc[t][1] = sload(rs, so1, ss);
+        const __amdgpu_buffer_rsrc_t rs = GATED && j == 1 ? rs_sl : rs_sg;
+        const int64_t ss = drow[j] * nblk * SB;
+#pragma unroll
+        for (int q = 0; q < NSC; ++q) {
+          const uint32_t so = kin ? soff + static_cast<uint32_t>(((k0 + q * (KH / NSC)) >> bshift) * SB) : kOob;
+          d.sc[j][q] = sload(rs, so, ss);
+        }
       }
     }
+  };
+
+  // Weight operand of block j, step s: 8 k as 16-bit values.
+  auto bop = [&](const Ring& d, int j, int s) -> u32x4_t {
+    u32x4_t q;
+    if constexpr (WF == kInt4) q = dq4_exact<AT>(d.w[j][s >> 2][s & 3]);
+    else if constexpr (WF == kInt8) q = dq8_exact<AT>(d.w[j][s >> 1][(s & 1) * 2], d.w[j][s >> 1][(s & 1) * 2 + 1]);
+    else q = d.w[j][s];
+    if constexpr (kFold) {
+      const float sc = d.sc[j][s * NSC / NSTEP];
+      if constexpr (AT::kId == 10 && ST::kId == 10) {
+        // fp16 scales: one packed multiply of the exact integers
+        const _Float16 sh = static_cast<_Float16>(sc);
+        const half2_t s2 = {sh, sh};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = h2_bits(bits_h2(q[r]) * s2);
+      } else {
+        if constexpr (WF == kInt4) q = dq4_scaled<AT>(d.w[j][s >> 2][s & 3], sc);
+        else q = dq8_scaled<AT>(d.w[j][s >> 1][(s & 1) * 2], d.w[j][s >> 1][(s & 1) * 2 + 1], sc);
+      }
+    }
+    return q;
   };
 
   // ---- activation stages go global -> LDS directly (buffer loads with the
@@ -246,44 +272,51 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
     }
   };
 
-  floatx4_t acc[kMT][kNT];
+  floatx16_t acc[kMT][kNT];
 #pragma unroll
   for (int i = 0; i < kMT; ++i)
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) acc[i][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // A operand of row tile i, step s: row m = 16 i + col, global piece
-  // gp0 + s; swz(m) does not depend on i
-  const int gp0 = KG * 2 * g / 16;
-  auto compute = [&](const uint8_t* buf, const Ring& d) {
+  // A operand of row block i, step s: row 32 i + lr, global piece
+  // (2 KH h + 16 s) / 16; swz(row) does not depend on i.
+  const uint8_t* arow0 = sA0 + lr * G::ROWB;
+  const uint8_t* arow1 = sA1 + lr * G::ROWB;
+  const int sw = G::swz(lr);
+  auto aread = [&](const uint8_t* arow, int s, int i) -> u32x4_t {
+    const int piece = ((KH * 2 * h + 16 * s) / 16) ^ sw;
+    return *reinterpret_cast<const u32x4_t*>(arow + i * 32 * G::ROWB + piece * 16);
+  };
+
+  // One stage, software pipelined over its steps: the activation reads and
+  // the dequantisation of step s + 1 are issued among the MFMAs of step s.
+  auto compute = [&](const uint8_t* arow, const Ring& d) {
+    u32x4_t a[kMT], b[kNT];
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) a[i] = aread(arow, 0, i);
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) b[j] = bop(d, j, 0);
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
-      const uint8_t* xa = buf + col * G::ROWB + ((gp0 + s) ^ G::swz(col)) * 16;
-      u32x4_t bw[kNT];
+      u32x4_t an[kMT], bn[kNT];
+      if (s + 1 < NSTEP) {
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        if constexpr (SM == kPsBlock && AT::kId == 10 && ST::kId == 10) {
-          // fp16: exact integers, then one packed multiply by the block scale
-          const u32x4_t q = weight_operand<AT, WF, false>(d.w[t], s, 0.0f);
-          const _Float16 sh = static_cast<_Float16>(d.sc[t][0]);
-          const half2_t s2 = {sh, sh};
+        for (int i = 0; i < kMT; ++i) an[i] = aread(arow, s + 1, i);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) bw[t][r] = h2_bits(bits_h2(q[r]) * s2);
-        } else if constexpr (kFold) {
-          const float sc = SM == kPsHalfBlock ? d.sc[t][s >> 1] : d.sc[t][0];
-          bw[t] = weight_operand<AT, WF, true>(d.w[t], s, sc);
-        } else {
-          bw[t] = weight_operand<AT, WF, false>(d.w[t], s, 0.0f);
-        }
+        for (int j = 0; j < kNT; ++j) bn[j] = bop(d, j, s + 1);
       }
 #pragma unroll
-      for (int i = 0; i < kMT; ++i) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xa + i * 16 * G::ROWB);
+      for (int i = 0; i < kMT; ++i)
 #pragma unroll
-        for (int t = 0; t < kNT; ++t) acc[i][t] = mfma16x16x32<AT>(a, bw[t], acc[i][t]);
+        for (int j = 0; j < kNT; ++j) acc[i][j] = mfma32x32x16<AT>(a[i], b[j], acc[i][j]);
+      if (s + 1 < NSTEP) {
+#pragma unroll
+        for (int i = 0; i < kMT; ++i) a[i] = an[i];
+#pragma unroll
+        for (int j = 0; j < kNT; ++j) b[j] = bn[j];
       }
-      // keep each step's operands next to its MFMAs (bounds live registers)
-      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -297,26 +330,29 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   fetch(0, ring[0]);
   __syncthreads();
   const int npairs = (nst + 1) / 2;
+  // The scheduling barriers keep the next stage's loads at the top of the
+  // stage (left alone, the scheduler sinks them next to the barrier, which
+  // then waits for their full latency).
   for (int q = 0; q < npairs; ++q) {
     const int c = 2 * q;
     aload(c + 1, sA1);
     fetch(c + 1, ring[1]);
-    compute(sA0, ring[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(arow0, ring[0]);
     __syncthreads();
     aload(c + 2, sA0);
     fetch(c + 2, ring[0]);
-    compute(sA1, ring[1]);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(arow1, ring[1]);
     __syncthreads();
   }
 
-  // ---- epilogue: lane holds D[16 i + 4 g + r][col] of tile (i, t) ----
+  // ---- epilogue: acc[i][j][q] is D[32 i + 8 (q / 4) + 4 h + q % 4][lr] ----
   const int act_t = AT::kId;
   if constexpr (FC1 && GATED) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int64_t f = fl + t * 16;
-      if (f >= p.nfeat) continue;
-      const int64_t rg = row0 + drow[t], rl = row0 + drow[t + 2];
+    const int64_t f = fl;
+    if (f < p.nfeat) {
+      const int64_t rg = row0 + drow[0], rl = row0 + drow[1];
       float chg = 1.0f, chl = 1.0f;
       if constexpr (SM == kPsChan) {
         chg = load_any(p.s, p.scale_type, static_cast<int64_t>(e) * p.w_rows + rg);
@@ -327,10 +363,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * i + 4 * g + r;
+        for (int q = 0; q < 16; ++q) {
+          const int m = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
           if (m >= rows) continue;
-          const float a = apply_act(acc[i][t][r] * chg + bg, acc[i][t + 2][r] * chl + bl, true, p.activation,
+          const float a = apply_act<true>(acc[i][0][q] * chg + bg, acc[i][1][q] * chl + bl, true, p.activation,
                                     p.alpha, p.beta, p.limit);
           static_cast<typename AT::storage*>(p.out)[static_cast<int64_t>(row_begin + m) * p.nfeat + f] =
               from_f32<AT>(a);
@@ -338,8 +374,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
     }
   } else {
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const int64_t f = fl + t * 16;
+    for (int j = 0; j < kNT; ++j) {
+      const int64_t f = fl + 32 * j;
       if (f >= p.nfeat) continue;
       float ch = 1.0f;
       if constexpr (SM == kPsChan) ch = load_any(p.s, p.scale_type, static_cast<int64_t>(e) * p.w_rows + f);
@@ -347,13 +383,13 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * i + 4 * g + r;
+        for (int q = 0; q < 16; ++q) {
+          const int m = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
           if (m >= rows) continue;
-          const float v = acc[i][t][r] * ch + bias;
+          const float v = acc[i][j][q] * ch + bias;
           const int64_t o = static_cast<int64_t>(row_begin + m) * p.nfeat + f;
           if constexpr (FC1) {
-            static_cast<typename AT::storage*>(p.out)[o] = from_f32<AT>(act_single(v, p.activation));
+            static_cast<typename AT::storage*>(p.out)[o] = from_f32<AT>(act_single<true>(v, p.activation));
           } else {
             static_cast<float*>(p.out)[static_cast<int64_t>(ks) * p.out_rows * p.nfeat + o] = v;
           }
@@ -362,27 +398,29 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   }
 }
 
-template <typename AT, int WF, int SM, typename ST, bool FC1>
+template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1>
 hipError_t launch_kernel(const PStage& st, bool gated, hipStream_t stream) {
   const unsigned nb = static_cast<unsigned>(st.ksplit) * st.ngroups * st.mslots * kGroupN;
   if (FC1 && gated)
-    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, true, true>), dim3(nb), dim3(256), 0, stream, st);
+    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, NSC, true, true>), dim3(nb), dim3(256), 0, stream, st);
   else
-    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, FC1, false>), dim3(nb), dim3(256), 0, stream, st);
+    hipLaunchKernelGGL((prefill_kernel<AT, WF, SM, ST, NSC, FC1, false>), dim3(nb), dim3(256), 0, stream, st);
   return hipGetLastError();
 }
 
 template <typename AT, int WF, bool FC1>
 hipError_t launch_scaled(const PStage& st, const ExpertArgs& a, bool gated, hipStream_t stream) {
   if constexpr (WF == kDense) {
-    return launch_kernel<AT, WF, kPsNone, F16, FC1>(st, gated, stream);
+    return launch_kernel<AT, WF, kPsNone, F16, 1, FC1>(st, gated, stream);
   } else {
-    if (a.block_size == 0) return launch_kernel<AT, WF, kPsChan, F16, FC1>(st, gated, stream);
-    const bool half = a.block_size < PG<WF>::KG;  // 16: two blocks per lane piece
+    if (a.block_size == 0) return launch_kernel<AT, WF, kPsChan, F16, 1, FC1>(st, gated, stream);
+    // scales per lane half and stage: KH / block_size (block_size >= 16)
+    const int64_t nsc = std::max<int64_t>(1, PG<WF>::KH / a.block_size);
     auto by_type = [&](auto st_tag) -> hipError_t {
       using ST = decltype(st_tag);
-      return half ? launch_kernel<AT, WF, kPsHalfBlock, ST, FC1>(st, gated, stream)
-                  : launch_kernel<AT, WF, kPsBlock, ST, FC1>(st, gated, stream);
+      if (nsc == 4) return launch_kernel<AT, WF, kPsBlock, ST, 4, FC1>(st, gated, stream);
+      if (nsc == 2) return launch_kernel<AT, WF, kPsBlock, ST, 2, FC1>(st, gated, stream);
+      return launch_kernel<AT, WF, kPsBlock, ST, 1, FC1>(st, gated, stream);
     };
     if (a.scale_type == MOE_ELEM_FLOAT) return by_type(F32{});
     if (a.scale_type == MOE_ELEM_BFLOAT16) return by_type(BF16{});
