@@ -165,32 +165,62 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   }
   const uint32_t woff = static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
 
-  // ---- per-block scales (folded): buffer loads of each block row's scales
-  // for the lane's k range; ranges past K or of a padding stage read 0 ----
+  // ---- per-block scales (folded).  Loading a 2-byte scale per lane and
+  // stage touches one cache line per row, as much address work as a weight
+  // load; so each wave instead loads windows of WB consecutive block scales
+  // of its 64 rows (block j = lane / 32, row lr: 16 bytes per lane), one
+  // window ahead, into a wave-private LDS area, and reads the scale of each
+  // stage from there.  Blocks past K (and padding stages) weigh 0. ----
   constexpr int SB = sizeof(typename ST::storage);
+  constexpr int WB = 16 / SB;  // blocks per window
   const int bshift = kFold ? __builtin_ctzll(static_cast<uint64_t>(p.block_size)) : 0;
-  const int64_t nblk = kFold ? (K >> bshift) : 0;
+  const int nblk = kFold ? (K >> bshift) : 0;
   const __amdgpu_buffer_rsrc_t rs_sg =
       make_rsrc(kFold ? static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk * SB : nullptr,
                 static_cast<uint32_t>(p.w_rows * nblk * SB));
   const __amdgpu_buffer_rsrc_t rs_sl =
       make_rsrc(kFold ? static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk * SB : nullptr,
                 static_cast<uint32_t>(p.wl_rows * nblk * SB));
-  const uint32_t soff = static_cast<uint32_t>(row0 * nblk * SB);
-  auto sload = [&](__amdgpu_buffer_rsrc_t r, uint32_t off, int64_t soffset) -> float {
-    if constexpr (SB == 4) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off),
-                                                                          static_cast<int>(soffset), 0));
-    } else {
-      const uint16_t v = __builtin_bit_cast(
-          uint16_t, __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), static_cast<int>(soffset), 0));
-      return to_f32<ST>(__builtin_bit_cast(typename ST::storage, v));
+  // this lane loads the scale row of block j = h, row lr
+  const uint32_t srow_off = static_cast<uint32_t>((row0 + drow[h]) * nblk * SB);
+  const bool s_aligned = (nblk * SB) % 16 == 0;
+  u32x4_t swin = {0u, 0u, 0u, 0u};  // window in flight (registers)
+  auto sfetch = [&](int m) {        // window m: blocks [WB m, WB m + WB)
+    if constexpr (kFold) {
+      const uint32_t o = srow_off + static_cast<uint32_t>(m * 16);
+      const uint32_t og = h == 0 ? o : kOob, ol = h == 1 ? o : kOob;
+      if (s_aligned) {
+        swin = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs_sg, static_cast<int>(og), 0, 0)) |
+               __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs_sl, static_cast<int>(ol), 0, 0));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rs_sg, static_cast<int>(og + 4 * q), 0, 0) |
+                              __builtin_amdgcn_raw_buffer_load_b16(rs_sl, static_cast<int>(ol + 4 * q), 0, 0);
+          const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rs_sg, static_cast<int>(og + 4 * q + 2), 0, 0) |
+                              __builtin_amdgcn_raw_buffer_load_b16(rs_sl, static_cast<int>(ol + 4 * q + 2), 0, 0);
+          swin[q] = lo | (hi << 16);
+        }
+      }
     }
+  };
+  // wave-private window buffers: [2][64 lanes][16 bytes]
+  __shared__ __attribute__((aligned(16))) uint8_t sS[kFold ? 4 * 2 * 64 * 16 : 16];
+  uint8_t* const swave = sS + (kFold ? wave * 2 * 64 * 16 : 0);
+  auto sstore = [&](int m) {
+    if constexpr (kFold) *reinterpret_cast<u32x4_t*>(swave + ((m & 1) * 64 + lane) * 16) = swin;
+  };
+  auto win_of = [&](int c) { return ((kbeg + c * BK) >> bshift) / WB; };  // window of stage c
+  // scale of block j for block index b (this lane's row), 0 past K
+  auto sread = [&](int j, int b) -> float {
+    const typename ST::storage* ent =
+        reinterpret_cast<const typename ST::storage*>(swave + (((b / WB) & 1) * 64 + j * 32 + lr) * 16);
+    const float v = to_f32<ST>(ent[b % WB]);
+    return b < nblk ? v : 0.0f;
   };
 
   struct Ring {
     u32x4_t w[kNT][BVEC];
-    float sc[kNT][kFold ? NSC : 1];
   };
   auto fetch = [&](int c, Ring& d) {
     const int k0 = kbeg + c * BK + KH * h;  // first k of the lane's range
@@ -204,26 +234,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       for (int v = 0; v < BVEC; ++v)
         d.w[j][v] = __builtin_bit_cast(
             u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw, 0));
-      if constexpr (kFold) {
-        const __amdgpu_buffer_rsrc_t rs = GATED && j == 1 ? rs_sl : rs_sg;
-        const int64_t ss = drow[j] * nblk * SB;
-#pragma unroll
-        for (int q = 0; q < NSC; ++q) {
-          const uint32_t so = kin ? soff + static_cast<uint32_t>(((k0 + q * (KH / NSC)) >> bshift) * SB) : kOob;
-          d.sc[j][q] = sload(rs, so, ss);
-        }
-      }
     }
   };
 
-  // Weight operand of block j, step s: 8 k as 16-bit values.
-  auto bop = [&](const Ring& d, int j, int s) -> u32x4_t {
+  // Weight operand of block j, step s: 8 k as 16-bit values; sc: the block
+  // scale of the step.
+  auto bop = [&](const Ring& d, int j, int s, float sc) -> u32x4_t {
     u32x4_t q;
     if constexpr (WF == kInt4) q = dq4_exact<AT>(d.w[j][s >> 2][s & 3]);
     else if constexpr (WF == kInt8) q = dq8_exact<AT>(d.w[j][s >> 1][(s & 1) * 2], d.w[j][s >> 1][(s & 1) * 2 + 1]);
     else q = d.w[j][s];
     if constexpr (kFold) {
-      const float sc = d.sc[j][s * NSC / NSTEP];
       if constexpr (AT::kId == 10 && ST::kId == 10) {
         // fp16 scales: one packed multiply of the exact integers
         const _Float16 sh = static_cast<_Float16>(sc);
@@ -292,12 +313,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 
   // One stage, software pipelined over its steps: the activation reads and
   // the dequantisation of step s + 1 are issued among the MFMAs of step s.
-  auto compute = [&](const uint8_t* arow, const Ring& d) {
+  auto compute = [&](int c, const uint8_t* arow, const Ring& d) {
+    // block scales of this stage: NSC per lane half and block j
+    float sc[kNT][NSC];
+#pragma unroll
+    for (int j = 0; j < kNT; ++j)
+#pragma unroll
+      for (int q = 0; q < NSC; ++q)
+        sc[j][q] = kFold ? sread(j, (kbeg + c * BK + KH * h + q * (KH / NSC)) >> bshift) : 1.0f;
     u32x4_t a[kMT], b[kNT];
 #pragma unroll
     for (int i = 0; i < kMT; ++i) a[i] = aread(arow, 0, i);
 #pragma unroll
-    for (int j = 0; j < kNT; ++j) b[j] = bop(d, j, 0);
+    for (int j = 0; j < kNT; ++j) b[j] = bop(d, j, 0, sc[j][0]);
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
       u32x4_t an[kMT], bn[kNT];
@@ -305,12 +333,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 #pragma unroll
         for (int i = 0; i < kMT; ++i) an[i] = aread(arow, s + 1, i);
 #pragma unroll
-        for (int j = 0; j < kNT; ++j) bn[j] = bop(d, j, s + 1);
+        for (int j = 0; j < kNT; ++j) bn[j] = bop(d, j, s + 1, sc[j][(s + 1) * NSC / NSTEP]);
       }
 #pragma unroll
       for (int i = 0; i < kMT; ++i)
 #pragma unroll
         for (int j = 0; j < kNT; ++j) acc[i][j] = mfma32x32x16<AT>(a[i], b[j], acc[i][j]);
+      // interleave: each MFMA followed by up to 4 VALU, a DS read every other
+#pragma unroll
+      for (int q = 0; q < kMT * kNT; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        if (q % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
       if (s + 1 < NSTEP) {
 #pragma unroll
         for (int i = 0; i < kMT; ++i) a[i] = an[i];
@@ -325,7 +360,24 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   // multiplied; the barrier after stage c waits for the LDS loads only (the
   // weight loads issued after them stay in flight).  A padding stage past the
   // split's range reads zeros. ----
+  // Scale windows: the first is stored before the loop, the next one is in
+  // flight; when stage c + 1 enters a new window, the in-flight one is stored
+  // (its buffer held the window before the current one) and the one after
+  // is requested.
+  auto swindow = [&](int c) {
+    if constexpr (kFold) {
+      if (win_of(c + 1) != win_of(c)) {
+        sstore(win_of(c + 1));
+        sfetch(win_of(c + 1) + 1);
+      }
+    }
+  };
   Ring ring[2];
+  if constexpr (kFold) {
+    sfetch(win_of(0));
+    sstore(win_of(0));
+    sfetch(win_of(0) + 1);
+  }
   aload(0, sA0);
   fetch(0, ring[0]);
   __syncthreads();
@@ -338,20 +390,40 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
     aload(c + 1, sA1);
     fetch(c + 1, ring[1]);
     __builtin_amdgcn_sched_barrier(0);
-    compute(arow0, ring[0]);
+    compute(c, arow0, ring[0]);
+    swindow(c);
     __syncthreads();
     aload(c + 2, sA0);
     fetch(c + 2, ring[0]);
     __builtin_amdgcn_sched_barrier(0);
-    compute(arow1, ring[1]);
+    compute(c + 1, arow1, ring[1]);
+    swindow(c + 1);
     __syncthreads();
   }
 
-  // ---- epilogue: acc[i][j][q] is D[32 i + 8 (q / 4) + 4 h + q % 4][lr] ----
+  // ---- epilogue: acc[i][j][q] is D[32 i + 8 (q / 4) + 4 h + q % 4][lr].
+  // Element offsets are 32-bit from the tile's first row; a full tile (the
+  // common case) stores without per-row checks. ----
   const int act_t = AT::kId;
+  const int nf = static_cast<int>(p.nfeat);  // nfeat * 128 < 2^31 (checked on the host)
+  auto for_rows = [&](auto&& emit) {
+    if (rows == BM) {
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) emit(i, q, 32 * i + 8 * (q >> 2) + 4 * h + (q & 3));
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int m = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
+          if (m < rows) emit(i, q, m);
+        }
+    }
+  };
   if constexpr (FC1 && GATED) {
-    const int64_t f = fl;
-    if (f < p.nfeat) {
+    if (fl < p.nfeat) {
       const int64_t rg = row0 + drow[0], rl = row0 + drow[1];
       float chg = 1.0f, chl = 1.0f;
       if constexpr (SM == kPsChan) {
@@ -360,17 +432,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       }
       const float bg = p.b ? load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + rg) : 0.0f;
       const float bl = p.bl ? load_any(p.bl, act_t, static_cast<int64_t>(e) * p.wl_rows + rl) : 0.0f;
-#pragma unroll
-      for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int m = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
-          if (m >= rows) continue;
-          const float a = apply_act<true>(acc[i][0][q] * chg + bg, acc[i][1][q] * chl + bl, true, p.activation,
-                                    p.alpha, p.beta, p.limit);
-          static_cast<typename AT::storage*>(p.out)[static_cast<int64_t>(row_begin + m) * p.nfeat + f] =
-              from_f32<AT>(a);
-        }
+      typename AT::storage* const op =
+          static_cast<typename AT::storage*>(p.out) + static_cast<int64_t>(row_begin) * p.nfeat + fl;
+      if (p.activation == kSwiglu) {
+        for_rows([&](int i, int q, int m) {
+          op[m * nf] = from_f32<AT>(swiglu_f<true>(acc[i][0][q] * chg + bg, acc[i][1][q] * chl + bl, p.alpha,
+                                                   p.beta, p.limit));
+        });
+      } else {
+        for_rows([&](int i, int q, int m) {
+          op[m * nf] = from_f32<AT>(apply_act<true>(acc[i][0][q] * chg + bg, acc[i][1][q] * chl + bl, true,
+                                                    p.activation, p.alpha, p.beta, p.limit));
+        });
+      }
     }
   } else {
 #pragma unroll
@@ -380,20 +454,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       float ch = 1.0f;
       if constexpr (SM == kPsChan) ch = load_any(p.s, p.scale_type, static_cast<int64_t>(e) * p.w_rows + f);
       const float bias = (p.b && ks == 0) ? load_any(p.b, act_t, static_cast<int64_t>(e) * p.w_rows + f) : 0.0f;
-#pragma unroll
-      for (int i = 0; i < kMT; ++i)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int m = 32 * i + 8 * (q >> 2) + 4 * h + (q & 3);
-          if (m >= rows) continue;
-          const float v = acc[i][j][q] * ch + bias;
-          const int64_t o = static_cast<int64_t>(row_begin + m) * p.nfeat + f;
-          if constexpr (FC1) {
-            static_cast<typename AT::storage*>(p.out)[o] = from_f32<AT>(act_single<true>(v, p.activation));
-          } else {
-            static_cast<float*>(p.out)[static_cast<int64_t>(ks) * p.out_rows * p.nfeat + o] = v;
-          }
-        }
+      if constexpr (FC1) {
+        typename AT::storage* const op =
+            static_cast<typename AT::storage*>(p.out) + static_cast<int64_t>(row_begin) * p.nfeat + f;
+        for_rows([&](int i, int q, int m) {
+          op[m * nf] = from_f32<AT>(act_single<true>(acc[i][j][q] * ch + bias, p.activation));
+        });
+      } else {
+        float* const op = static_cast<float*>(p.out) + static_cast<int64_t>(ks) * p.out_rows * p.nfeat +
+                          static_cast<int64_t>(row_begin) * p.nfeat + f;
+        for_rows([&](int i, int q, int m) { op[m * nf] = acc[i][j][q] * ch + bias; });
+      }
     }
   }
 }
@@ -477,6 +548,7 @@ bool prefill_supported(const ExpertArgs& a) {
   const int64_t n1 = (a.gate_mode == kGateInterleaved || a.gate_mode == kGateChunked) ? 2 * a.I : a.I;
   if (n1 * a.H * ebits / 8 >= lim || a.H * a.I * ebits / 8 >= lim) return false;
   if (a.T * a.k * std::max(a.H, a.I) * 2 >= lim) return false;
+  if (std::max(a.H, a.I) * BM >= lim) return false;  // 32-bit in-tile offsets of the epilogue
   return true;
 }
 
