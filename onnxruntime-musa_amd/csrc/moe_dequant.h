@@ -94,33 +94,42 @@ __device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
   const half2_t h = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
   return h2_bits(h);
 }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 template <>
 __device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2_t h = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};  // one v_cvt_pk_bf16_f32
+  return __builtin_bit_cast(uint32_t, h);
 }
 
-// Scaled converters: 8 weights times per-element-group scale s -> 16-bit.
+// Scaled converters: 8 weights times per-element-group scale s -> 16-bit,
+// one rounding of (q - zp) * s: the byte converts exactly to fp32 and one
+// fma against the exact constant -zp * s (zp is a power of two) forms the
+// product.
 template <typename AT>
 __device__ __forceinline__ u32x4_t dq4_scaled(uint32_t v, float s) {
+  const uint32_t x = v & 0x0F0F0F0Fu;         // k0, k2, k4, k6
+  const uint32_t y = (v >> 4) & 0x0F0F0F0Fu;  // k1, k3, k5, k7
+  const float ns = -8.0f * s;
   u32x4_t r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    const uint32_t byte = (v >> (8 * b)) & 0xFFu;
-    r[b] = pack2<AT>((static_cast<float>(byte & 0xFu) - 8.0f) * s,
-                     (static_cast<float>(byte >> 4) - 8.0f) * s);
+    const float lo = static_cast<float>((x >> (8 * b)) & 0xFFu);  // v_cvt_f32_ubyte<b>
+    const float hi = static_cast<float>((y >> (8 * b)) & 0xFFu);
+    r[b] = pack2<AT>(__builtin_fmaf(lo, s, ns), __builtin_fmaf(hi, s, ns));
   }
   return r;
 }
 
 template <typename AT>
 __device__ __forceinline__ u32x4_t dq8_scaled(uint32_t v0, uint32_t v1, float s) {
+  const float ns = -128.0f * s;
   u32x4_t r;
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
-    r[b] = pack2<AT>((static_cast<float>((v0 >> (16 * b)) & 0xFFu) - 128.0f) * s,
-                     (static_cast<float>((v0 >> (16 * b + 8)) & 0xFFu) - 128.0f) * s);
-    r[2 + b] = pack2<AT>((static_cast<float>((v1 >> (16 * b)) & 0xFFu) - 128.0f) * s,
-                         (static_cast<float>((v1 >> (16 * b + 8)) & 0xFFu) - 128.0f) * s);
+    r[b] = pack2<AT>(__builtin_fmaf(static_cast<float>((v0 >> (16 * b)) & 0xFFu), s, ns),
+                     __builtin_fmaf(static_cast<float>((v0 >> (16 * b + 8)) & 0xFFu), s, ns));
+    r[2 + b] = pack2<AT>(__builtin_fmaf(static_cast<float>((v1 >> (16 * b)) & 0xFFu), s, ns),
+                         __builtin_fmaf(static_cast<float>((v1 >> (16 * b + 8)) & 0xFFu), s, ns));
   }
   return r;
 }

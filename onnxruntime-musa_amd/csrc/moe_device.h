@@ -27,11 +27,10 @@ struct BF16 { using storage = uint16_t; static constexpr int kId = 16; };
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
+// Round to nearest even (gfx950 converts in hardware, v_cvt_pk_bf16_f32; NaN
+// stays a quiet NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t x = __float_as_uint(f);
-  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((x >> 16) | 0x40u);
-  x += 0x7FFFu + ((x >> 16) & 1u);
-  return static_cast<uint16_t>(x >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 template <typename Tag>
