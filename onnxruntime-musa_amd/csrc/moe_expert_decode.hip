@@ -51,16 +51,20 @@ void pick_splits(Stage& st, const ExpertArgs& a, bool gated, bool allow_ksg) {
   st.lds_scale = static_cast<int32_t>((lds_per_wave(ks * ksg) + 15) / 16 * 16);
 }
 
+// Host mirror of LGeo: chunks the LDS kernel walks at a time (RD pieces of
+// PC chunks); a K group other than the last is a multiple of it.
+inline int64_t lds_unit(int wfmt) { return wfmt == kDense ? 3 : 4; }
+
 // K groups of the fc2 LDS kernel: more groups while fewer than ~512
 // workgroups would stream weights (experts expected to be hit times feature
 // groups) and each group keeps at least two pieces of 4 chunks.  fc1 always
-// uses one group.  K per group is a multiple of a piece (4 chunks).
-void lds_groups(int64_t K, int64_t fgroups, int64_t e_act, bool split, int32_t* ksg, int32_t* kr) {
+// uses one group.  K per group is a multiple of the kernel's unit.
+void lds_groups(int64_t K, int64_t fgroups, int64_t e_act, bool split, int64_t unit, int32_t* ksg, int32_t* kr) {
   const int64_t nchunks = (K + kChunk - 1) / kChunk;
   int64_t g = 1;
   while (split && e_act * fgroups * g < 512 && nchunks / (2 * g) >= 8 && 2 * g <= kMaxLdsKsplit) g *= 2;
   int64_t per = (nchunks + g - 1) / g;
-  per = (per + 3) / 4 * 4;
+  per = (per + unit - 1) / unit * unit;
   *ksg = static_cast<int32_t>((nchunks + per - 1) / per);
   *kr = static_cast<int32_t>(per * kChunk);
 }
@@ -92,7 +96,6 @@ hipError_t dispatch_lds(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool 
 
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode) {
   DecodePlan pl;
-  (void)wfmt;
   if (T > kDecodeMaxTokens) return pl;
   const bool gated = gate_mode != kGateNone;
   pl.y2_planes_max = kMaxDecodeKsplit;
@@ -106,8 +109,8 @@ DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, in
   pl.lds = e_act * pl.fgroups1 >= 256;
   pl.lds2 = true;
   const int64_t fgroups2 = (H + 64 * ft2 - 1) / (64 * ft2);
-  decode::lds_groups(H, pl.fgroups1, e_act, false, &pl.ksg1, &pl.kr1);
-  decode::lds_groups(I, fgroups2, e_act, true, &pl.ksg2, &pl.kr2);
+  decode::lds_groups(H, pl.fgroups1, e_act, false, decode::lds_unit(wfmt), &pl.ksg1, &pl.kr1);
+  decode::lds_groups(I, fgroups2, e_act, true, decode::lds_unit(wfmt), &pl.ksg2, &pl.kr2);
   pl.y2_planes_max = std::max<int32_t>(pl.ksg2, kMaxDecodeKsplit);
   return pl;
 }

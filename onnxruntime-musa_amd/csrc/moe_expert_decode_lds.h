@@ -40,8 +40,10 @@ struct LGeo {
   static constexpr int kLaneBytes = 16 * kVecs;
   static constexpr int FT = GATED ? 1 : 2;  // feature tiles per wave
   static constexpr int WT = 2;              // weight tiles per wave
-  static constexpr int PD = WF == kDense ? 3 : 4;
-  static constexpr int PC = PD;                       // chunks per staged piece
+  static constexpr int PC = WF == kDense ? 3 : 4;      // chunks per staged piece
+  static constexpr int RD = 1;                         // pieces of weights in flight (2 measured slower:
+                                                       // the deeper ring costs a wave per SIMD)
+  static constexpr int PD = RD * PC;                   // register ring depth (chunks)
   static constexpr int kPitch = PC * kChunk * 2 + 16;  // LDS row pitch, bytes (16-byte skew)
   static constexpr int kBuf = kLdsRows * kPitch;       // one staged piece
 };
@@ -54,7 +56,7 @@ struct LChunk {
 template <typename AT, int WF, int SM, typename ST, bool FC1, bool GATED>
 __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
   using G = LGeo<WF, GATED>;
-  constexpr int WT = G::WT, FT = G::FT, PD = G::PD, PC = G::PC, LB = G::kLaneBytes;
+  constexpr int WT = G::WT, FT = G::FT, PD = G::PD, PC = G::PC, RD = G::RD, LB = G::kLaneBytes;
   constexpr bool kPerBlock = SM == kScaleBlock || SM == kScaleFold;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const Stage& p = ls.s;
@@ -144,9 +146,10 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
 
   // Start the weight stream before staging, so the first chunks are in flight
   // while the first activation piece is copied.
-  // The K range is walked in whole pieces of PC chunks; chunks past c1 are
-  // padding that reads nothing and multiplies zeros.
-  const int npieces = (c1 - c0 + PC - 1) / PC;
+  // The K range is walked in whole groups of RD pieces of PC chunks; chunks
+  // past c1 are padding that reads nothing and multiplies zeros (a K group
+  // other than the last is a whole number of such groups).
+  const int npieces = (c1 - c0 + RD * PC - 1) / (RD * PC) * RD;
   const int cend = c0 + npieces * PC;
   CK ring[PD];
 #pragma unroll
@@ -182,17 +185,28 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
   floatx4_t acc[WT];
 #pragma unroll
   for (int t = 0; t < WT; ++t) acc[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  // biased weights (block scales of whole chunks, or per-channel scales):
+  // sx collects the activation sums that remove the bias
+  constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan);
+  constexpr float kOff = Biased<AT, WF>::kOffset;
+  const u32x4_t ones = {Biased<AT, WF>::kOnes, Biased<AT, WF>::kOnes, Biased<AT, WF>::kOnes, Biased<AT, WF>::kOnes};
+  floatx4_t sx = {0.f, 0.f, 0.f, 0.f};
   const int b0i = static_cast<int>(b0);  // K < 2^31: block indices fit 32 bits
 
   auto compute = [&](int c, int buf, int cin, const CK& d) {
     floatx4_t tmp[WT];
 #pragma unroll
     for (int t = 0; t < WT; ++t) tmp[t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    floatx4_t sxc = {0.f, 0.f, 0.f, 0.f};
     const uint8_t* xc = smem + buf * G::kBuf + col * G::kPitch + g * 64 + cin * (kChunk * 2);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       // rows past the expert's token count were staged as zeros
       const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xc + 16 * s);
+      if constexpr (kBiased) {
+        if constexpr (SM == kScaleBlock) sxc = mfma16x16x32<AT>(a, ones, sxc);
+        else sx = mfma16x16x32<AT>(a, ones, sx);
+      }
 #pragma unroll
       for (int t = 0; t < WT; ++t) {
         float fs = 0.0f;
@@ -200,7 +214,9 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
           const int blk = ((c * kChunk + 32 * g + 8 * s) >> bshift) - b0i;
           fs = sc[(t * nb + blk) * 16 + col];
         }
-        const u32x4_t bw = weight_operand<AT, WF, SM == kScaleFold>(d.w[t], s, fs);
+        u32x4_t bw;
+        if constexpr (kBiased) bw = weight_biased<AT, WF>(d.w[t], s);
+        else bw = weight_operand<AT, WF, SM == kScaleFold>(d.w[t], s, fs);
         if constexpr (SM == kScaleBlock) tmp[t] = mfma16x16x32<AT>(a, bw, tmp[t]);
         else acc[t] = mfma16x16x32<AT>(a, bw, acc[t]);
       }
@@ -208,29 +224,43 @@ __global__ void __launch_bounds__(256) gemv_lds_kernel(LdsStage ls) {
     if constexpr (SM == kScaleBlock) {
       const int blk = ((c * kChunk) >> bshift) - b0i;
 #pragma unroll
-      for (int t = 0; t < WT; ++t) acc[t] += tmp[t] * sc[(t * nb + blk) * 16 + col];
+      for (int t = 0; t < WT; ++t) {
+        floatx4_t v = tmp[t];
+        if constexpr (kBiased) v -= kOff * sxc;
+        acc[t] += v * sc[(t * nb + blk) * 16 + col];
+      }
     }
   };
 
   // Pieces of PC = PD chunks: piece q uses LDS buffer q % 2 and ring slots
   // 0..PC-1; the next piece's activations are loaded during the piece and
   // stored behind it, then one barrier closes the piece.
-  for (int q = 0; q < npieces; ++q) {
-    const int cq = c0 + q * PC;
-    const bool more = q + 1 < npieces;
-    if (more) xload(q + 1);
+  // With RD > 1 the ring spans RD pieces: piece q uses slots (q % RD) * PC
+  // onward, so pieces are walked RD at a time to keep slot indices static.
+  for (int q0 = 0; q0 < npieces; q0 += RD) {
 #pragma unroll
-    for (int d = 0; d < PC; ++d) {
-      compute(cq + d, q & 1, d, ring[d]);
-      fetch(min(cq + d + PD, cend - 1), ring[d]);
-      // keep each chunk's LDS reads and dequantisation next to its MFMAs
-      __builtin_amdgcn_sched_barrier(0);
+    for (int r = 0; r < RD; ++r) {
+      const int q = q0 + r;
+      const int cq = c0 + q * PC;
+      const bool more = q + 1 < npieces;
+      if (more) xload(q + 1);
+#pragma unroll
+      for (int d = 0; d < PC; ++d) {
+        compute(cq + d, q & 1, d, ring[r * PC + d]);
+        fetch(min(cq + d + PD, cend - 1), ring[r * PC + d]);
+        // keep each chunk's LDS reads and dequantisation next to its MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (more) xstore((q + 1) & 1);
+      __syncthreads();
     }
-    if (more) xstore((q + 1) & 1);
-    __syncthreads();
   }
 
   // ---- epilogue ----
+  if constexpr (kBiased && SM == kScaleChan) {
+#pragma unroll
+    for (int t = 0; t < WT; ++t) acc[t] -= kOff * sx;
+  }
   const int act_t = AT::kId;
   if constexpr (!FC1) {
     // fc2: this K group's plane of y2 (bias in plane 0)

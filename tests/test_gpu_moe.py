@@ -64,6 +64,21 @@ def test_quant_formats(cuda, q, dtype, path, T):
     check_problem(p, path)
 
 
+@pytest.mark.parametrize("base,over", [
+    (C5, dict(hidden=256, inter=3072, experts=8, k=2)),
+    (C3, dict(hidden=256, inter=4096)),
+    (C2, dict(hidden=256, inter=4096)),
+    (C4, dict(hidden=256, inter=2880, experts=8)),
+], ids=["dense", "int4", "int8", "int4-bs32-bf16"])
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_decode_long_k_groups(cuda, base, over, T):
+    """Few experts and a long fc2 K: the decode path splits K across
+    workgroups into partial planes (K groups are whole multiples of the
+    kernel's chunk walk; the last one is padded past K)."""
+    p = make_problem(base, T, seed=11 + T, device=cuda, gen="numpy", **over)
+    check_problem(p, "decode")
+
+
 ACTS = [
     dict(activation="relu", use_fc3=False),
     dict(activation="gelu", use_fc3=False),
