@@ -1,9 +1,11 @@
 // moe_expert_decode.hip -- host launchers of the decode (weight-streaming)
-// expert kernels.  Up to kLdsMaxTokens tokens the activation rows are staged
-// in LDS (moe_expert_decode_lds.h); up to kDecodeMaxTokens they are read from
-// global memory (moe_expert_decode.h).  The quantised instantiations live in
-// moe_expert_decode_int4.hip / _int8.hip.
-#include "moe_expert_decode_lds.h"
+// expert kernels.  Up to kLdsMaxTokens tokens, persistent workgroups stage
+// the activation rows in LDS (moe_expert_stream.h); up to kDecodeMaxTokens
+// the rows are read from global memory (moe_expert_decode.h).  The quantised
+// instantiations live in moe_expert_decode_int4.hip / _int8.hip.
+#include <atomic>
+
+#include "moe_expert_stream.h"
 
 namespace moe {
 namespace decode {
@@ -14,13 +16,24 @@ hipError_t launch_dense(const Stage& st, const ExpertArgs& a, bool fc1, bool gat
   return launch_kinds<F16, kDense, kScaleNone, F16>(st, a.T, a.E, fc1, gated, stream);
 }
 
-hipError_t launch_lds_dense(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
-  return launch_lds_fmt<kDense>(ls, a, fc1, gated, stream);
+hipError_t launch_stream_dense(const StreamStage& ss, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+  return launch_stream_fmt<kDense>(ss, a, fc1, gated, stream);
+}
+
+// One persistent workgroup per CU of the current device (cached per device).
+int stream_grid(int /*nw*/) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 namespace {
-
-constexpr int kMaxLdsKsplit = 32;
 
 // Splits of K for the global-activation kernel: ks waves inside a workgroup
 // and, for fc2, ksg workgroups (partial output planes summed by finalize).
@@ -51,28 +64,20 @@ void pick_splits(Stage& st, const ExpertArgs& a, bool gated, bool allow_ksg) {
   st.lds_scale = static_cast<int32_t>((lds_per_wave(ks * ksg) + 15) / 16 * 16);
 }
 
-// Host mirror of LGeo: chunks the LDS kernel walks at a time (RD pieces of
-// PC chunks); a K group other than the last is a multiple of it.
-inline int64_t lds_unit(int wfmt) { return wfmt == kDense ? 3 : 4; }
-
-// K groups of the fc2 LDS kernel: more groups while fewer than ~512
-// workgroups would stream weights (experts expected to be hit times feature
-// groups) and each group keeps at least two pieces of 4 chunks.  fc1 always
-// uses one group.  K per group is a multiple of the kernel's unit.
-void lds_groups(int64_t K, int64_t fgroups, int64_t e_act, bool split, int64_t unit, int32_t* ksg, int32_t* kr) {
+// K slices of the stream kernel: as few as fit the LDS slice, each a whole
+// number of ring blocks (pd chunks).  Equal slices without padding are
+// preferred (e.g. 112 chunks: 7 x 16 rather than 4 x 32 with the last half
+// empty); otherwise the last slice is padded.
+void stream_slices(int64_t K, int pd, int32_t* nsl, int32_t* ksc) {
   const int64_t nchunks = (K + kChunk - 1) / kChunk;
-  int64_t g = 1;
-  while (split && e_act * fgroups * g < 512 && nchunks / (2 * g) >= 8 && 2 * g <= kMaxLdsKsplit) g *= 2;
-  int64_t per = (nchunks + g - 1) / g;
-  per = (per + unit - 1) / unit * unit;
-  *ksg = static_cast<int32_t>((nchunks + per - 1) / per);
-  *kr = static_cast<int32_t>(per * kChunk);
-}
-
-int64_t lds_scale_bytes(int64_t kr, int64_t block_size) {
-  if (block_size == 0) return 0;
-  const int64_t nb = (kr + block_size - 1) / block_size + 1;
-  return (2 * 16 * nb * 4 + 15) / 16 * 16;  // 2 weight tiles per wave
+  const int64_t maxper = kStreamMaxChunks / pd * pd;
+  const int64_t nmin = (nchunks + maxper - 1) / maxper;
+  int64_t per = 0;
+  for (int64_t n = nmin; n < nmin + 8 && per == 0; ++n)
+    if (nchunks % n == 0 && (nchunks / n) % pd == 0) per = nchunks / n;
+  if (per == 0) per = ((nchunks + nmin - 1) / nmin + pd - 1) / pd * pd;
+  *nsl = static_cast<int32_t>((nchunks + per - 1) / per);
+  *ksc = static_cast<int32_t>(per);
 }
 
 hipError_t dispatch(const Stage& st, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
@@ -83,11 +88,11 @@ hipError_t dispatch(const Stage& st, const ExpertArgs& a, bool fc1, bool gated, 
   }
 }
 
-hipError_t dispatch_lds(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+hipError_t dispatch_stream(const StreamStage& ss, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
   switch (a.wfmt) {
-    case kInt4: return launch_lds_int4(ls, a, fc1, gated, stream);
-    case kInt8: return launch_lds_int8(ls, a, fc1, gated, stream);
-    default: return launch_lds_dense(ls, a, fc1, gated, stream);
+    case kInt4: return launch_stream_int4(ss, a, fc1, gated, stream);
+    case kInt8: return launch_stream_int8(ss, a, fc1, gated, stream);
+    default: return launch_stream_dense(ss, a, fc1, gated, stream);
   }
 }
 
@@ -95,23 +100,19 @@ hipError_t dispatch_lds(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool 
 }  // namespace decode
 
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode) {
+  (void)E;
+  (void)k;
+  (void)gate_mode;
   DecodePlan pl;
   if (T > kDecodeMaxTokens) return pl;
-  const bool gated = gate_mode != kGateNone;
   pl.y2_planes_max = kMaxDecodeKsplit;
   if (T > kLdsMaxTokens) return pl;
-  const int64_t e_act = std::min<int64_t>(E, T * k);
-  const int64_t ft1 = gated ? 1 : 2, ft2 = 2;
-  pl.fgroups1 = static_cast<int32_t>((I + 64 * ft1 - 1) / (64 * ft1));
-  // fc1 cannot split K across workgroups, so it stages activations in LDS
-  // only when its feature groups alone give at least one workgroup per CU;
-  // fc2 splits K as needed.
-  pl.lds = e_act * pl.fgroups1 >= 256;
-  pl.lds2 = true;
-  const int64_t fgroups2 = (H + 64 * ft2 - 1) / (64 * ft2);
-  decode::lds_groups(H, pl.fgroups1, e_act, false, decode::lds_unit(wfmt), &pl.ksg1, &pl.kr1);
-  decode::lds_groups(I, fgroups2, e_act, true, decode::lds_unit(wfmt), &pl.ksg2, &pl.kr2);
-  pl.y2_planes_max = std::max<int32_t>(pl.ksg2, kMaxDecodeKsplit);
+  // fc1 streams only when its whole K fits one LDS slice; fc2 always streams
+  decode::stream_slices(H, decode::stream_pd(wfmt), &pl.nsl1, &pl.ksc1);
+  decode::stream_slices(I, decode::stream_pd(wfmt), &pl.nsl2, &pl.ksc2);
+  pl.stream1 = pl.nsl1 == 1;
+  pl.stream2 = true;
+  pl.y2_planes_max = std::max<int32_t>(pl.nsl2, kMaxDecodeKsplit);
   return pl;
 }
 
@@ -200,14 +201,13 @@ hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
   const bool gated = a.gate_mode != kGateNone;
   decode::Stage st = fc1_stage(a);
   const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
-  if (pl.lds) {
-    decode::LdsStage ls{};
-    ls.s = st;
-    ls.s.ks = 1;
-    ls.s.ksg = pl.ksg1;
-    ls.kr = pl.kr1;
-    ls.s.lds_scale = static_cast<int32_t>(decode::lds_scale_bytes(pl.kr1, st.block_size));
-    return decode::dispatch_lds(ls, a, true, gated, stream);
+  if (pl.stream1) {
+    decode::StreamStage ss{};
+    ss.s = st;
+    ss.ksc = pl.ksc1;
+    ss.nslices = 1;
+    ss.E = static_cast<int32_t>(a.E);
+    return decode::dispatch_stream(ss, a, true, gated, stream);
   }
   decode::pick_splits(st, a, gated, false);
   return decode::dispatch(st, a, true, gated, stream);
@@ -216,15 +216,14 @@ hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
 hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream) {
   decode::Stage st = fc2_stage(a);
   const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
-  if (pl.lds2) {
-    decode::LdsStage ls{};
-    ls.s = st;
-    ls.s.ks = 1;
-    ls.s.ksg = pl.ksg2;
-    ls.kr = pl.kr2;
-    ls.s.lds_scale = static_cast<int32_t>(decode::lds_scale_bytes(pl.kr2, st.block_size));
-    *y2_planes = pl.ksg2;
-    return decode::dispatch_lds(ls, a, false, false, stream);
+  if (pl.stream2) {
+    decode::StreamStage ss{};
+    ss.s = st;
+    ss.ksc = pl.ksc2;
+    ss.nslices = pl.nsl2;
+    ss.E = static_cast<int32_t>(a.E);
+    *y2_planes = pl.nsl2;
+    return decode::dispatch_stream(ss, a, false, false, stream);
   }
   decode::pick_splits(st, a, false, true);
   *y2_planes = st.ksg;

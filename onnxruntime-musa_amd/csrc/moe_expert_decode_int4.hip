@@ -1,6 +1,6 @@
 // moe_expert_decode_int4.hip -- int4 instantiations of the decode expert kernels
-// (kernel templates: moe_expert_decode.h, moe_expert_decode_lds.h).
-#include "moe_expert_decode_lds.h"
+// (kernel templates: moe_expert_decode.h, moe_expert_stream.h).
+#include "moe_expert_stream.h"
 
 namespace moe {
 namespace decode {
@@ -9,8 +9,8 @@ hipError_t launch_int4(const Stage& st, const ExpertArgs& a, bool fc1, bool gate
   return launch_quant<kInt4>(st, a, fc1, gated, stream);
 }
 
-hipError_t launch_lds_int4(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
-  return launch_lds_fmt<kInt4>(ls, a, fc1, gated, stream);
+hipError_t launch_stream_int4(const StreamStage& ss, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+  return launch_stream_fmt<kInt4>(ss, a, fc1, gated, stream);
 }
 
 }  // namespace decode

@@ -1,6 +1,6 @@
 // moe_expert_decode_int8.hip -- int8 instantiations of the decode expert kernels
-// (kernel templates: moe_expert_decode.h, moe_expert_decode_lds.h).
-#include "moe_expert_decode_lds.h"
+// (kernel templates: moe_expert_decode.h, moe_expert_stream.h).
+#include "moe_expert_stream.h"
 
 namespace moe {
 namespace decode {
@@ -9,8 +9,8 @@ hipError_t launch_int8(const Stage& st, const ExpertArgs& a, bool fc1, bool gate
   return launch_quant<kInt8>(st, a, fc1, gated, stream);
 }
 
-hipError_t launch_lds_int8(const LdsStage& ls, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
-  return launch_lds_fmt<kInt8>(ls, a, fc1, gated, stream);
+hipError_t launch_stream_int8(const StreamStage& ss, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
+  return launch_stream_fmt<kInt8>(ss, a, fc1, gated, stream);
 }
 
 }  // namespace decode

@@ -95,10 +95,10 @@ constexpr int kMaxDecodeKsplit = 8;
 // Launch plan of the decode kernels, shared by the workspace planner and the
 // launchers so both agree on the partial-plane sizes.
 struct DecodePlan {
-  bool lds = false;         // fc1: activation slice staged in LDS
-  bool lds2 = false;        // fc2: activation slice staged in LDS
-  int32_t ksg1 = 1, kr1 = 0, fgroups1 = 0;  // fc1 K groups, K per group, feature groups
-  int32_t ksg2 = 1, kr2 = 0;                // fc2 K groups, K per group
+  bool stream1 = false;  // fc1: persistent kernel, activation slice staged in LDS
+  bool stream2 = false;  // fc2: persistent kernel
+  int32_t nsl1 = 1, ksc1 = 0;  // fc1 K slices, chunks of 128 k per slice
+  int32_t nsl2 = 1, ksc2 = 0;  // fc2 K slices (partial planes of y2), chunks per slice
   int32_t y2_planes_max = 1;
 };
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode);
