@@ -72,7 +72,7 @@ struct SGeo {
   static constexpr int kLaneBytes = 16 * kVecs;                           // bytes per 32 k of a row
   static constexpr int FT = GATED ? 1 : 2;                                // 16-feature tiles per tile
   static constexpr int WT = 2;                                            // 16-row weight tiles per tile
-  static constexpr int NW = 8;                                            // waves per workgroup
+  static constexpr int NW = WF == kInt4 ? 12 : 8;                         // waves per workgroup
   static constexpr int PD = WF == kDense ? 4 : 8;                         // ring depth (chunks)
 };
 
