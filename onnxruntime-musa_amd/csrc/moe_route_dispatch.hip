@@ -234,7 +234,7 @@ __global__ void __launch_bounds__(1024) route_dispatch_small_kernel(RouteArgs a)
 
 // ---- large T, pass 1: route + per-workgroup histogram ----
 template <typename LT, int VPL>
-__global__ void __launch_bounds__(256) route_hist_kernel(RouteArgs a, int32_t* hist) {
+__global__ void __launch_bounds__(1024) route_hist_kernel(RouteArgs a, int32_t* hist) {
   __shared__ int cnt[kMaxExperts];
   const moe_route_params& p = a.p;
   const int E = static_cast<int>(p.num_experts), k = static_cast<int>(p.k);
@@ -260,27 +260,59 @@ __global__ void __launch_bounds__(256) route_hist_kernel(RouteArgs a, int32_t* h
 }
 
 // ---- large T, pass 2: one workgroup scans the histograms ----
-// hist[b][e] becomes the first row of expert e owned by workgroup b.
+// hist[b][e] becomes the first row of expert e owned by workgroup b.  The
+// 1024 threads split each expert's column of nblocks counts into parts
+// (threads e + E * part); a thread reads its part in register chunks of 16
+// independent loads, so the column is read at memory bandwidth rather than
+// one dependent load at a time.
+constexpr int kScanChunk = 16;
+
 __global__ void __launch_bounds__(1024) dispatch_scan_kernel(RouteArgs a, int32_t* hist,
                                                              int nblocks) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int base[kMaxExperts];
+  __shared__ int psum[1024];
   const int E = static_cast<int>(a.p.num_experts);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  const int parts = blockDim.x / E;  // E <= kMaxExperts <= blockDim.x
+  const int tid = threadIdx.x;
+  const int e = tid % E, part = tid / E;
+  const bool active = part < parts;
+  const int per = (nblocks + parts - 1) / parts;
+  const int b0 = active ? part * per : 0;
+  const int b1 = active ? min(nblocks, b0 + per) : 0;
+  // column sums of each part
+  int sum = 0;
+  for (int c = b0; c < b1; c += kScanChunk) {
+    int v[kScanChunk];
+#pragma unroll
+    for (int j = 0; j < kScanChunk; ++j) v[j] = c + j < b1 ? hist[static_cast<int64_t>(c + j) * E + e] : 0;
+#pragma unroll
+    for (int j = 0; j < kScanChunk; ++j) sum += v[j];
+  }
+  psum[tid] = sum;
+  __syncthreads();
+  if (tid < E) {
     int run = 0;
-    for (int b = 0; b < nblocks; ++b) {
-      const int c = hist[static_cast<int64_t>(b) * E + e];
-      hist[static_cast<int64_t>(b) * E + e] = run;
-      run += c;
-    }
-    cnt[e] = run;
+    for (int q = 0; q < parts; ++q) run += psum[q * E + tid];
+    cnt[tid] = run;
   }
   __syncthreads();
   scan_experts(cnt, E, base, a.p.offsets, a.tile_offsets, a.tile_m);
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    const int off = base[e];
-    for (int b = 0; b < nblocks; ++b) hist[static_cast<int64_t>(b) * E + e] += off;
+  // exclusive running sums, starting at the expert's base plus earlier parts
+  if (active) {
+    int run = base[e];
+    for (int q = 0; q < part; ++q) run += psum[q * E + e];
+    for (int c = b0; c < b1; c += kScanChunk) {
+      int v[kScanChunk];
+#pragma unroll
+      for (int j = 0; j < kScanChunk; ++j) v[j] = c + j < b1 ? hist[static_cast<int64_t>(c + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < kScanChunk; ++j) {
+        if (c + j < b1) hist[static_cast<int64_t>(c + j) * E + e] = run;
+        run += v[j];
+      }
+    }
   }
 }
 
@@ -308,7 +340,8 @@ hipError_t launch_typed(const RouteArgs& a, hipStream_t stream) {
   }
   const int nblocks = static_cast<int>((T + kRouteTokensPerBlock - 1) / kRouteTokensPerBlock);
   int32_t* hist = static_cast<int32_t*>(a.p.scratch);
-  hipLaunchKernelGGL((route_hist_kernel<LT, VPL>), dim3(nblocks), dim3(256), 0, stream, a, hist);
+  // 16 waves per workgroup: 4 tokens per wave
+  hipLaunchKernelGGL((route_hist_kernel<LT, VPL>), dim3(nblocks), dim3(1024), 0, stream, a, hist);
   hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(1024), 0, stream, a, hist, nblocks);
   hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(nblocks), dim3(256), 0, stream, a,
                      static_cast<const int32_t*>(hist));
