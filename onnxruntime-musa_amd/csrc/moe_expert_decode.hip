@@ -64,22 +64,6 @@ void pick_splits(Stage& st, const ExpertArgs& a, bool gated, bool allow_ksg) {
   st.lds_scale = static_cast<int32_t>((lds_per_wave(ks * ksg) + 15) / 16 * 16);
 }
 
-// K slices of the stream kernel: as few as fit the LDS slice, each a whole
-// number of ring blocks (pd chunks).  Equal slices without padding are
-// preferred (e.g. 112 chunks: 7 x 16 rather than 4 x 32 with the last half
-// empty); otherwise the last slice is padded.
-void stream_slices(int64_t K, int pd, int32_t* nsl, int32_t* ksc) {
-  const int64_t nchunks = (K + kChunk - 1) / kChunk;
-  const int64_t maxper = kStreamMaxChunks / pd * pd;
-  const int64_t nmin = (nchunks + maxper - 1) / maxper;
-  int64_t per = 0;
-  for (int64_t n = nmin; n < nmin + 8 && per == 0; ++n)
-    if (nchunks % n == 0 && (nchunks / n) % pd == 0) per = nchunks / n;
-  if (per == 0) per = ((nchunks + nmin - 1) / nmin + pd - 1) / pd * pd;
-  *nsl = static_cast<int32_t>((nchunks + per - 1) / per);
-  *ksc = static_cast<int32_t>(per);
-}
-
 hipError_t dispatch(const Stage& st, const ExpertArgs& a, bool fc1, bool gated, hipStream_t stream) {
   switch (a.wfmt) {
     case kInt4: return launch_int4(st, a, fc1, gated, stream);

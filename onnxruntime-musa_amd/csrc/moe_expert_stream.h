@@ -57,7 +57,7 @@ constexpr int kStreamMaxChunks = 36;  // K chunks of one staged slice (16 x 36 x
 constexpr int kStreamFetch = 4;       // chunks whose loads are issued back to back
 
 // Chunks per block (= register ring depth); a K slice is a whole number of blocks.
-inline int stream_pd(int wfmt) { return wfmt == kDense ? 4 : 8; }
+inline int stream_pd(int wfmt) { return wfmt == kInt4 ? 8 : 4; }
 
 struct StreamStage {
   Stage s;
@@ -72,8 +72,8 @@ struct SGeo {
   static constexpr int kLaneBytes = 16 * kVecs;                           // bytes per 32 k of a row
   static constexpr int FT = GATED ? 1 : 2;                                // 16-feature tiles per tile
   static constexpr int WT = 2;                                            // 16-row weight tiles per tile
-  static constexpr int NW = WF == kInt4 ? 12 : 8;                         // waves per workgroup
-  static constexpr int PD = WF == kDense ? 4 : 8;                         // ring depth (chunks)
+  static constexpr int NW = WF == kDense ? 8 : 12;                         // waves per workgroup
+  static constexpr int PD = WF == kInt4 ? 8 : 4;                         // ring depth (chunks)
 };
 
 // Raw block scales of one lane: NSC consecutive elements in one load.
@@ -119,6 +119,22 @@ struct SChunk {
 __device__ __forceinline__ u32x4_t dq4_f16_split(uint32_t v, uint32_t m_lo, uint32_t m_hi) {
   const uint32_t c = 0x64006400u, h = v >> 8;
   return u32x4_t{(v & m_lo) | c, (v & m_hi) | c, (h & m_lo) | c, (h & m_hi) | c};
+}
+
+// K slices of the stream kernel: as few as fit the LDS slice, each a whole
+// number of ring blocks (pd chunks).  Equal slices without padding are
+// preferred (e.g. 112 chunks: 7 x 16 rather than 4 x 32 with the last half
+// empty); otherwise the last slice is padded.
+inline void stream_slices(int64_t K, int pd, int32_t* nsl, int32_t* ksc) {
+  const int64_t nchunks = (K + kChunk - 1) / kChunk;
+  const int64_t maxper = kStreamMaxChunks / pd * pd;
+  const int64_t nmin = (nchunks + maxper - 1) / maxper;
+  int64_t per = 0;
+  for (int64_t n = nmin; n < nmin + 8 && per == 0; ++n)
+    if (nchunks % n == 0 && (nchunks / n) % pd == 0) per = nchunks / n;
+  if (per == 0) per = ((nchunks + nmin - 1) / nmin + pd - 1) / pd * pd;
+  *nsl = static_cast<int32_t>((nchunks + per - 1) / per);
+  *ksc = static_cast<int32_t>(per);
 }
 
 // Bytes of dynamic LDS of the stream kernel.
