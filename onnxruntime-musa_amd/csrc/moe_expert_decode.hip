@@ -191,6 +191,7 @@ hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
     ss.ksc = pl.ksc1;
     ss.nslices = 1;
     ss.E = static_cast<int32_t>(a.E);
+    ss.ngroups = decode::stream_groups(a.T, a.E, a.k);
     return decode::dispatch_stream(ss, a, true, gated, stream);
   }
   decode::pick_splits(st, a, gated, false);
@@ -206,6 +207,7 @@ hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t st
     ss.ksc = pl.ksc2;
     ss.nslices = pl.nsl2;
     ss.E = static_cast<int32_t>(a.E);
+    ss.ngroups = decode::stream_groups(a.T, a.E, a.k);
     *y2_planes = pl.nsl2;
     return decode::dispatch_stream(ss, a, false, false, stream);
   }

@@ -1,6 +1,8 @@
-// moe_expert_stream.h -- decode expert GEMV for up to 16 token rows per
-// expert: one persistent workgroup per CU streams an even share of the
-// weight tiles of all routed experts.
+// moe_expert_stream.h -- decode expert GEMV (up to 64 tokens): one
+// persistent workgroup per CU streams an even share of the weight tiles of
+// all routed experts.  An expert's rows are taken in groups of 16 (the MFMA
+// M dimension); an expert with more than 16 rows streams its weights once
+// per group.
 //
 // Why persistent: a decode layer reads each routed expert's weights once, and
 // the unit a launch grid hands out (a feature group with its whole K) is too
@@ -9,7 +11,7 @@
 // CUs empty.  Here every workgroup takes the same number of weight tiles
 // (+-1) and its waves split those tiles' K chunks evenly.
 //
-// Work space: tiles are (routed expert a, K slice s, feature tile f), f
+// Work space: tiles are (row group a, K slice s, feature tile f), f
 // fastest.  A tile is 16 features (gate + linear rows when gated) or 32
 // features (two 16-row weight tiles), over KSC chunks of 128 k.  Workgroup i
 // takes tiles [T*i/P, T*(i+1)/P).  A run of its tiles with the same (a, s) is
@@ -64,6 +66,7 @@ struct StreamStage {
   int32_t ksc;      // chunks per K slice (multiple of the ring depth; the last slice is padded)
   int32_t nslices;  // K slices (fc2 partial planes)
   int32_t E;        // experts
+  int32_t ngroups;  // bound on the row groups of all experts: E + T*k/16
 };
 
 template <int WF, bool GATED>
@@ -137,9 +140,16 @@ inline void stream_slices(int64_t K, int pd, int32_t* nsl, int32_t* ksc) {
   *ksc = static_cast<int32_t>(per);
 }
 
-// Bytes of dynamic LDS of the stream kernel.
-inline size_t stream_lds_bytes(int ksc, int E, int nw) {
-  const size_t ex = (static_cast<size_t>(E) * 4 + 15) / 16 * 16;
+// Bound on the row groups (16 rows of one expert) of a call: each routed
+// expert has at most one partial group.
+inline int32_t stream_groups(int64_t T, int64_t E, int64_t k) {
+  const int64_t rows = T * k;
+  return static_cast<int32_t>(std::min(E, rows) + (rows + kStreamRows - 1) / kStreamRows);
+}
+
+// Bytes of dynamic LDS of the stream kernel (ngroups: row-group list entries).
+inline size_t stream_lds_bytes(int ksc, int ngroups, int nw) {
+  const size_t ex = (static_cast<size_t>(ngroups) * 4 + 15) / 16 * 16;
   const size_t act = static_cast<size_t>(kStreamRows) * (static_cast<size_t>(ksc) * 256 + 16) +
                      static_cast<size_t>(ksc) * kStreamRows * 4;
   const size_t slots = static_cast<size_t>(nw) * 2 * 64 * 16;
@@ -170,19 +180,27 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   const int col = lane & 15, g = lane >> 4;
   const int ksc = ss.ksc, nsl = ss.nslices, E = ss.E;
   const int pitch = ksc * 256 + 16;
-  int* exl = reinterpret_cast<int*>(smem);  // routed experts, ascending
-  uint8_t* region = smem + (E * 4 + 15) / 16 * 16;
+  int* exl = reinterpret_cast<int*>(smem);  // row groups: expert | (group << 16), ascending
+  uint8_t* region = smem + (ss.ngroups * 4 + 15) / 16 * 16;
   uint8_t* xs = region;                                         // [16][pitch] activation slice
   float* corr = reinterpret_cast<float*>(region + 16 * pitch);  // [ksc][16] bias sums per chunk and row
   float* slots = reinterpret_cast<float*>(region);              // [NW][WT][64] float4, after the compute
 
-  // ---- routed experts: exl[0 .. e_act) ----
+  // ---- row groups: each routed expert's rows in groups of 16 (the MFMA M);
+  // an expert with more rows streams its weights once per group.
+  // exl[0 .. e_act) ----
   int e_act = 0;
   for (int base = 0; base < E; base += NT) {
     const int e = base + tid;
-    const bool on = e < E && p.offsets[e + 1] > p.offsets[e];
-    const uint64_t m = __ballot(on);
-    if (lane == 0) wcount[wave] = __popcll(m);
+    const int cnt = e < E ? p.offsets[e + 1] - p.offsets[e] : 0;
+    const int nv = (cnt + kStreamRows - 1) / kStreamRows;
+    int inc = nv;  // inclusive scan over the wave
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += t;
+    }
+    if (lane == kWave - 1) wcount[wave] = inc;
     __syncthreads();
     int before = 0, total = 0;
     for (int w = 0; w < NW; ++w) {
@@ -190,9 +208,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       before += w < wave ? c : 0;
       total += c;
     }
-    const int below = static_cast<int>(__builtin_amdgcn_mbcnt_hi(
-        static_cast<uint32_t>(m >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u)));
-    if (on) exl[e_act + before + below] = e;
+    const int x0 = e_act + before + inc - nv;
+    for (int j = 0; j < nv; ++j) exl[x0 + j] = e | (j << 16);
     e_act += total;
     __syncthreads();
   }
@@ -253,8 +270,9 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int ntl = static_cast<int>(t_end - t < nft - f0 ? t_end - t : nft - f0);
     const int nb = ntl * bpt;
     const int b0 = nb * wave / NW, b1 = nb * (wave + 1) / NW;
-    const int e = __builtin_amdgcn_readfirstlane(exl[a]);
-    const int row0 = __builtin_amdgcn_readfirstlane(p.offsets[e]);
+    const int ent = __builtin_amdgcn_readfirstlane(exl[a]);
+    const int e = ent & 0xFFFF;
+    const int row0 = __builtin_amdgcn_readfirstlane(p.offsets[e]) + (ent >> 16) * kStreamRows;
     const int cnt = __builtin_amdgcn_readfirstlane(p.offsets[e + 1]) - row0;
     const int nrows = cnt < kStreamRows ? cnt : kStreamRows;
     const int cs0 = s * ksc;  // first chunk of the slice
@@ -564,7 +582,7 @@ template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATE
 hipError_t launch_stream(const StreamStage& ss, hipStream_t stream) {
   using G = SGeo<WF, GATED>;
   auto kern = gemv_stream_kernel<AT, WF, SM, ST, NSC, FC1, GATED>;
-  const size_t lds = stream_lds_bytes(ss.ksc, ss.E, G::NW);  // <= 152 KB of gfx950's 160 KB
+  const size_t lds = stream_lds_bytes(ss.ksc, ss.ngroups, G::NW);  // <= 152 KB + the group list
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(stream_grid(G::NW))), dim3(G::NW * 64), lds, stream, ss);
   return hipGetLastError();
 }

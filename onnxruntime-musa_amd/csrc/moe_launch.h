@@ -87,8 +87,9 @@ int32_t prefill_fc2_splits(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k
 constexpr int kPrefillTileM = 128;
 // Largest token count served by the decode (weight-streaming) path.
 constexpr int64_t kDecodeMaxTokens = 64;
-// Token count up to which decode stages the activation rows in LDS.
-constexpr int64_t kLdsMaxTokens = 16;
+// Token count up to which decode stages the activation rows in LDS (in
+// groups of 16 rows per expert).
+constexpr int64_t kLdsMaxTokens = 64;
 // Most K splits across workgroups of the decode fc2 kernel (partial planes of y2).
 constexpr int kMaxDecodeKsplit = 8;
 
