@@ -87,6 +87,7 @@ struct PStage {
   int32_t ntiles;   // weight tiles of BN rows (gated: BN/2 features)
   int32_t ngroups;  // ceil(ntiles / kGroupN)
   int32_t ksplit;   // K splits (partial planes of the output)
+  int32_t out_half; // fc2 with one plane: y2 stored in the activation type
   int32_t kstages;  // stages per K split
   int64_t out_rows;
   void* out;  // fc1: act [rows, nfeat] (AT); fc2: y2 [ksplit][rows, nfeat] fp32
@@ -455,6 +456,10 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
         for_rows([&](int i, int q, int m) {
           op[m * nf] = from_f32<AT>(act_single<true>(acc[i][j][q] * ch + bias, p.activation));
         });
+      } else if (p.out_half) {
+        typename AT::storage* const op =
+            static_cast<typename AT::storage*>(p.out) + static_cast<int64_t>(row_begin) * p.nfeat + f;
+        for_rows([&](int i, int q, int m) { op[m * nf] = from_f32<AT>(acc[i][j][q] * ch + bias); });
       } else {
         float* const op = static_cast<float*>(p.out) + static_cast<int64_t>(ks) * p.out_rows * p.nfeat +
                           static_cast<int64_t>(row_begin) * p.nfeat + f;
@@ -589,7 +594,7 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream) {
   return launch_stage<true>(st, a, gated, stream);
 }
 
-hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, hipStream_t stream) {
+hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half, hipStream_t stream) {
   PStage st{};
   st.in = a.act;
   st.in_rows = a.T * a.k;
@@ -616,7 +621,11 @@ hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, hipStream_t s
   st.out = a.y2;
   const int32_t splits = prefill_fc2_splits(a.T, a.H, a.I, a.E, a.k, a.wfmt);
   plan_grid(st, a.T, a.k, a.E, a.wfmt, a.H, splits);
+  // fp16 and one plane: y2 goes out in fp16 (one rounding of the expert
+  // output before the fp32 weighted sum; half the bytes written and read)
+  st.out_half = splits == 1 && a.act_type == MOE_ELEM_FLOAT16 ? 1 : 0;
   *y2_planes = splits;
+  *y2_half = st.out_half;
   return launch_stage<false>(st, a, false, stream);
 }
 

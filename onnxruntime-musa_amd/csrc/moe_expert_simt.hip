@@ -107,6 +107,25 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   const int64_t h0 = (static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x) * 4;
   if (h0 >= a.H) return;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.y2_half) {  // one fp16 plane
+    const _Float16* y2h = reinterpret_cast<const _Float16*>(a.y2);
+    for (int64_t j = 0; j < a.k; ++j) {
+      const int64_t f = t * a.k + j;
+      const float w = a.topk_w[f];
+      const _Float16* y = y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H;
+      if (h0 + 4 <= a.H && (a.H % 4) == 0) {  // 8-byte aligned: one load of 4 values
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        const half4_t v = *reinterpret_cast<const half4_t*>(y + h0);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += w * static_cast<float>(v[c]);
+      } else {
+        for (int c = 0; c < 4 && h0 + c < a.H; ++c) acc[c] += w * static_cast<float>(y[h0 + c]);
+      }
+    }
+    typename OT::storage* out = static_cast<typename OT::storage*>(a.out);
+    for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
+    return;
+  }
   for (int64_t j = 0; j < a.k; ++j) {
     const int64_t f = t * a.k + j;
     const float w = a.topk_w[f];

@@ -65,6 +65,7 @@ struct ExpertArgs {
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
   int32_t y2_planes;
+  int32_t y2_half;  // 1: y2 is one plane of fp16 values (fp16 prefill without a K split)
   void* out;   // [T, H] act_type
 };
 
@@ -73,7 +74,7 @@ hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
 hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
-hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
+hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half, hipStream_t stream);
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
 
 // Whether the MFMA paths accept this problem (fp16/bf16 activations, K a

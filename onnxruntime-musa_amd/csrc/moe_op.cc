@@ -292,6 +292,7 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
   a.y2_planes = 1;
+  a.y2_half = 0;
   a.out = output;
   return a;
 }
@@ -501,7 +502,7 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
       case moe::kPathPrefill:
         e = moe::launch_fc1_prefill(a, stream);
         mark(2);
-        if (e == hipSuccess) e = moe::launch_fc2_prefill(a, &a.y2_planes, stream);
+        if (e == hipSuccess) e = moe::launch_fc2_prefill(a, &a.y2_planes, &a.y2_half, stream);
         break;
       default:
         e = moe::launch_fc1_simt(a, stream);
