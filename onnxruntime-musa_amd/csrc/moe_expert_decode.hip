@@ -86,14 +86,13 @@ hipError_t dispatch_stream(const StreamStage& ss, const ExpertArgs& a, bool fc1,
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode) {
   (void)E;
   (void)k;
-  (void)gate_mode;
   DecodePlan pl;
   if (T > kDecodeMaxTokens) return pl;
   pl.y2_planes_max = kMaxDecodeKsplit;
   if (T > kLdsMaxTokens) return pl;
   // fc1 streams only when its whole K fits one LDS slice; fc2 always streams
-  decode::stream_slices(H, decode::stream_pd(wfmt), &pl.nsl1, &pl.ksc1);
-  decode::stream_slices(I, decode::stream_pd(wfmt), &pl.nsl2, &pl.ksc2);
+  decode::stream_slices(H, decode::stream_pd(wfmt, gate_mode != kGateNone), &pl.nsl1, &pl.ksc1);
+  decode::stream_slices(I, decode::stream_pd(wfmt, false), &pl.nsl2, &pl.ksc2);
   pl.stream1 = pl.nsl1 == 1;
   pl.stream2 = true;
   pl.y2_planes_max = std::max<int32_t>(pl.nsl2, kMaxDecodeKsplit);
