@@ -28,9 +28,8 @@
 //
 // Weights stream through a register ring of PD chunks (one block): each
 // chunk of the next block is requested as soon as the same slot of the
-// current block is consumed, and a group's first block is requested before
-// its activation slice is staged.  Block scales travel in the ring beside
-// the weights.
+// current block is consumed, and a group's first block is requested while
+// its activation slice is staged.
 //
 // Biased operands: int8/int4 weights enter the MFMA with their zero point
 // and magic-exponent bias still in (1024 + q for fp16, 128 + q for bf16),
@@ -55,13 +54,15 @@ namespace moe {
 namespace decode {
 
 constexpr int kStreamRows = 16;       // token rows staged (the MFMA M dimension)
-constexpr int kStreamMaxChunks = 36;  // K chunks of one staged slice (16 x 36 x 256 B of LDS)
+constexpr int kStreamMaxChunks = 32;  // K chunks of one staged slice (16 x 32 x 256 B of LDS)
 constexpr int kStreamFetch = 4;       // chunks whose loads are issued back to back
 
-// Chunks per block (= register ring depth); a K slice is a whole number of
-// blocks.  8 only for gated int4 (fc1 + fc3): fc2's 7 KB rows measured 6%
-// faster with 4.
-inline int stream_pd(int wfmt, bool gated) { return wfmt == kInt4 && gated ? 8 : 4; }
+// Chunks per block; a K slice is a whole number of blocks.
+inline int stream_pd(int wfmt, bool gated) {
+  (void)wfmt;
+  (void)gated;
+  return 4;
+}
 
 struct StreamStage {
   Stage s;
@@ -78,8 +79,13 @@ struct SGeo {
   static constexpr int FT = GATED ? 1 : 2;                                // 16-feature tiles per tile
   static constexpr int WT = 2;                                            // 16-row weight tiles per tile
   static constexpr int NW = WF == kDense ? 8 : 12;                         // waves per workgroup
-  static constexpr int PD = WF == kInt4 && GATED ? 8 : 4;                         // ring depth (chunks)
+  static constexpr int PD = 4;                                              // chunks per block (ring depth)
 };
+
+// s_waitcnt operand that waits until at most n (< 64) vector memory
+// operations are outstanding and leaves expcnt and lgkmcnt alone (gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 
 // Raw block scales of one lane: NSC consecutive elements in one load.
 template <typename ST, int NSC>
@@ -169,7 +175,18 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   constexpr bool kSplit = kBiased && WF == kInt4 && AT::kId == 10;
   constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold;
   constexpr bool kGroupScales = SM == kScaleBlock && NSC == 4;
+  // 2-byte block scales of block 128 are loaded per tile: one load per
+  // lane (row col, lane group g) brings the 16 bytes that hold the scales
+  // of the slice's chunks 8g .. 8g + 7 (a slice has at most 32 chunks), and
+  // each block hands its 4 chunks' scales to the lanes of the row with one
+  // cross-lane read per 2 chunks.  One request per row and tile, where
+  // per-block loads would touch every row's cache line again for each
+  // block of the tile.  The load for a tile is issued during the block
+  // before it, after that block has read the previous tile's scales.
+  constexpr bool kTileScales = kGroupScales && sizeof(typename ST::storage) == 2;
+  static_assert(!kTileScales || kStreamMaxChunks <= 32, "a slice's scales are 4 x 16 bytes per row");
   static_assert(PD % kStreamFetch == 0, "a block is whole fetch groups");
+  static_assert(!(SM == kScaleBlock && NSC == 4) || PD % 4 == 0, "grouped scales: 4 chunks of one block");
   using SR = ScaleRaw<ST, NSC>;
   using CK = SChunk<WF, GATED, SR, kRingScales>;
   constexpr int kEs = static_cast<int>(sizeof(typename ST::storage));
@@ -235,7 +252,6 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     nblk = static_cast<uint32_t>(K >> bshift);
   }
   const __amdgpu_buffer_rsrc_t rs_x = make_rsrc(p.in, static_cast<uint32_t>(p.in_rows * K * 2));
-  const int act_t = AT::kId;
   const int nfeat = static_cast<int>(p.nfeat);
 
   // Weight row of feature f in weight tile u: f * rmul + radd[u] (gate rows
@@ -303,6 +319,20 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       }
     };
     CK ring[PD];
+    // tile scales of the current (or, late in its last block, the next) tile
+    u32x4_t tsr[WT];
+    auto fetch_tsc = [&](int tl) {
+      if constexpr (kTileScales) {
+        uint32_t woff[WT], soff[WT];
+        tile_offs(tl, woff, soff);
+#pragma unroll
+        for (int u = 0; u < WT; ++u)
+          tsr[u] = bload16(GATED && u >= FT ? ss_l : ss_g, soff[u] + static_cast<uint32_t>(cs0) * 2 + 16 * g);
+      }
+    };
+    // vector memory loads that fetching one block issues
+    constexpr int kBlockLoads =
+        PD * WT * G::kVecs + (kTileScales ? 0 : (kRingScales ? (kGroupScales ? PD / 4 : PD) * WT : 0));
     auto fetch = [&](int cl, const uint32_t* woff, const uint32_t* soff, CK& d) {
       const int cg = cs0 + cl;
       // padding chunks past K and the missing lanes of a partial last chunk
@@ -315,7 +345,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         const uint32_t o = (woff[u] + wc) | oob;
 #pragma unroll
         for (int v = 0; v < G::kVecs; ++v) d.w[u][v] = bload16(GATED && u >= FT ? rs_l : rs_g, o + 16 * v);
-        if constexpr (kRingScales) {
+        if constexpr (kRingScales && !kTileScales) {
           const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (SM == kScaleFold ? 32 * g : 0);
           // a block scale multiplies the whole chunk's sum (every lane group
           // of the MFMA output), so only a chunk past K reads none
@@ -326,78 +356,92 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       }
     };
 
-    // ---- first block of this wave's run, then the activation slice ----
-    if (b0 < b1) {
+    // ---- the group's activation slice goes global -> LDS directly (buffer
+    // loads with the LDS bit): one 16-byte piece per lane, 1 KB per wave
+    // instruction, which is 64 consecutive pieces of one row (a row of the
+    // slice is ksc * 16 pieces and ksc is a multiple of 4).  Group q goes to
+    // wave q % NW.  k past K reads zeros.  These loads go out before the
+    // weight loads, so that staging waits for one round trip and not behind
+    // the weights that every workgroup requests at the same moment. ----
+    const int gpr = ksc / 4;        // 1 KB groups per row
+    const int ngr = nrows * gpr;    // groups of the slice
+    // source row of row m (fc1: the token of dispatched row row0 + m), lane m
+    const int srcl = FC1 ? (lane < nrows ? static_cast<int>(p.perm[row0 + lane] / p.topk) : 0) : row0 + lane;
+    for (int q = wave; q < ngr; q += NW) {
+      const int m = q / gpr, r = (q - m * gpr) * 64 + lane;  // row, piece in the row
+      const int64_t k = static_cast<int64_t>(cs0 + (r >> 4)) * kChunk + (r & 15) * 8;
+      const int64_t src = __builtin_amdgcn_readlane(srcl, m);
+      const uint32_t off = k < K ? static_cast<uint32_t>((src * K + k) * 2) : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs_x, (__attribute__((address_space(3))) void*)(xs + m * pitch + (r - lane) * 16), 16,
+          static_cast<int>(off), 0, 0, 0);
+    }
+    // the first tile's scales (before the weights, so that waiting for them
+    // does not wait for the weights)
+    fetch_tsc(b0 / bpt);
+    // The first block of the run.  Every wave issues its loads (with an
+    // empty run they read nothing), so that the run loop is always entered
+    // with the same loads in flight as at its back edge and its waits stay
+    // one block deep.
+    {
       uint32_t woff[WT], soff[WT];
       const int tl = b0 / bpt, cb = b0 - tl * bpt;
       tile_offs(tl, woff, soff);
+      if (b0 >= b1) {
+#pragma unroll
+        for (int u = 0; u < WT; ++u) woff[u] = soff[u] = kOob;
+      }
 #pragma unroll
       for (int d = 0; d < PD; ++d) fetch(cb * PD + d, woff, soff, ring[d]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    {
-      // rounds of kJ 16-byte pieces per thread: loads first, then transform and store
-      constexpr int kJ = 3;
-      const int per_row = ksc * 16;  // 16-byte pieces per row
-      const int npc = nrows * per_row;
-      for (int i0 = 0; i0 < npc; i0 += NT * kJ) {
-        u32x4_t xv[kJ];
+    // This wave's slice pieces have landed once no more than the weight
+    // loads issued after them are in flight (the compiler does not order a
+    // wave's LDS reads after its own LDS-bound loads).
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(kBlockLoads));
+    // Each wave finishes the pieces it loaded: the int4 split (odd k / 16
+    // and the k order of the weights) in place, and the bias sums per
+    // (chunk, row) of biased operands (the 16 pieces of one (row, chunk) sit
+    // in 16 consecutive lanes).
+    if constexpr (kBiased) {
+      for (int q = wave; q < ngr; q += NW) {
+        const int m = q / gpr, r = (q - m * gpr) * 64 + lane;
+        u32x4_t* px = reinterpret_cast<u32x4_t*>(xs + m * pitch + r * 16);
+        u32x4_t y = *px;
+        float cs = 0.0f;
+        if constexpr (kSplit) {
+          const half2_t q16 = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
+          const u32x4_t x = y;
+          y[0] = __builtin_amdgcn_perm(x[2], x[0], 0x05040100u);
+          y[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(x[2], x[0], 0x07060302u)) * q16);
+          y[2] = __builtin_amdgcn_perm(x[3], x[1], 0x05040100u);
+          y[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(x[3], x[1], 0x07060302u)) * q16);
+          float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          const int i = i0 + tid + NT * j;
-          uint32_t off = kOob;
-          if (i < npc) {
-            const int m = i / per_row, r = i - m * per_row;
-            const int64_t k = static_cast<int64_t>(cs0 + (r >> 4)) * kChunk + (r & 15) * 8;
-            const int64_t src = FC1 ? p.perm[row0 + m] / p.topk : row0 + m;
-            if (k < K) off = static_cast<uint32_t>((src * K + k) * 2);
+          for (int c = 0; c < 4; ++c) {
+            const half2_t h = bits_h2(y[c]);
+            const float v = static_cast<float>(h[0]) + static_cast<float>(h[1]);
+            if (c & 1) hi += v;
+            else lo += v;
           }
-          xv[j] = bload16(rs_x, off);
+          cs = 1032.0f * lo + 1152.0f * hi;
+          *px = y;
+        } else {
+          float sum = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if constexpr (AT::kId == 10) {
+              const half2_t h = bits_h2(y[c]);
+              sum += static_cast<float>(h[0]) + static_cast<float>(h[1]);
+            } else {
+              sum += __uint_as_float(y[c] << 16) + __uint_as_float(y[c] & 0xFFFF0000u);
+            }
+          }
+          cs = Biased<AT, WF>::kOffset * sum;
         }
 #pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-          const int i = i0 + tid + NT * j;
-          u32x4_t y = xv[j];
-          float cs = 0.0f;
-          if constexpr (kSplit) {
-            const half2_t q16 = {static_cast<_Float16>(0.0625f), static_cast<_Float16>(0.0625f)};
-            const u32x4_t x = xv[j];
-            y[0] = __builtin_amdgcn_perm(x[2], x[0], 0x05040100u);
-            y[1] = h2_bits(bits_h2(__builtin_amdgcn_perm(x[2], x[0], 0x07060302u)) * q16);
-            y[2] = __builtin_amdgcn_perm(x[3], x[1], 0x05040100u);
-            y[3] = h2_bits(bits_h2(__builtin_amdgcn_perm(x[3], x[1], 0x07060302u)) * q16);
-            float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const half2_t h = bits_h2(y[q]);
-              const float v = static_cast<float>(h[0]) + static_cast<float>(h[1]);
-              if (q & 1) hi += v;
-              else lo += v;
-            }
-            cs = 1032.0f * lo + 1152.0f * hi;
-          } else if constexpr (kBiased) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if constexpr (AT::kId == 10) {
-                const half2_t h = bits_h2(y[q]);
-                sum += static_cast<float>(h[0]) + static_cast<float>(h[1]);
-              } else {
-                sum += __uint_as_float(y[q] << 16) + __uint_as_float(y[q] & 0xFFFF0000u);
-              }
-            }
-            cs = Biased<AT, WF>::kOffset * sum;
-          }
-          if constexpr (kBiased) {
-            // the 16 pieces of one (row, chunk) sit in 16 consecutive lanes
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) cs += __shfl_xor(cs, o, kWave);
-          }
-          if (i < npc) {
-            const int m = i / per_row, r = i - m * per_row;
-            *reinterpret_cast<u32x4_t*>(xs + m * pitch + r * 16) = y;
-            if (kBiased && (r & 15) == 0) corr[(r >> 4) * kStreamRows + m] = cs;
-          }
-        }
+        for (int o = 1; o < 16; o <<= 1) cs += __shfl_xor(cs, o, kWave);
+        if ((r & 15) == 0) corr[(r >> 4) * kStreamRows + m] = cs;
       }
     }
     __syncthreads();
@@ -415,6 +459,9 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       lead[u] = acc[u];
     }
 
+    // tile scales of the current block's 4 chunks (chunk d: half d & 1 of
+    // bsc[u][d >> 1])
+    u32x2_t bsc[WT];
     auto compute = [&](int cl, int slot) {
       const CK& d = ring[slot];
       floatx4_t tmp[WT];
@@ -445,33 +492,67 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         if constexpr (kBiased) cr = *reinterpret_cast<const floatx4_t*>(corr + cl * kStreamRows + 4 * g);
 #pragma unroll
         for (int u = 0; u < WT; ++u) {
-          const float sc = kGroupScales ? SR::elem(ring[slot & ~3].sc[u], slot & 3) : SR::elem(d.sc[u], 0);
+          float sc;
+          if constexpr (kTileScales) sc = SR::elem(bsc[u], slot & (PD - 1));
+          else if constexpr (kGroupScales) sc = SR::elem(ring[slot & ~3].sc[u], slot & 3);
+          else sc = SR::elem(d.sc[u], 0);
           acc[u] += (tmp[u] - cr) * sc;
         }
       }
     };
 
-    // Per-channel scales and biases of tile tl (ep[u], ep[WT + u] for weight
-    // tile u), requested when a tile's first block starts so that finishing
-    // it never waits behind the weight stream.
-    auto load_ep = [&](int tl, float* ep) {
+    // Raw bits of the per-channel scales and biases of tile tl (weight tile
+    // u: scale ep[u] and, for fp32 scales, its upper half ep[2 WT + u]; bias
+    // ep[WT + u]), requested when a tile's first block starts and converted
+    // in finish.  The loads are branch-free (features past the end and
+    // absent biases read nothing, as 0) and nothing uses them before the
+    // tile ends, so that no wait for them sits in front of the weight stream.
+    const int ses = p.scale_type == MOE_ELEM_FLOAT ? 4 : 2;
+    auto load_ep = [&](int tl, uint32_t* ep) {
       const int ft = f0 + tl;
 #pragma unroll
       for (int u = 0; u < WT; ++u) {
         const bool lin = GATED && u >= FT;
-        ep[u] = 1.0f;
-        ep[WT + u] = 0.0f;
-        if (ft * (16 * FT) + fo[u] < nfeat) {
-          const int64_t ri = static_cast<int64_t>(e) * (lin ? p.wl_rows : p.w_rows) + ft * (16 * FT * rmul) + rowb[u];
-          if constexpr (SM == kScaleChan) ep[u] = load_any(lin ? p.sl : p.s, p.scale_type, ri);
-          const void* bp = lin ? p.bl : p.b;
-          if (bp && (FC1 || s == 0)) ep[WT + u] = load_any(bp, act_t, ri);
+        const int64_t rows = lin ? p.wl_rows : p.w_rows;
+        const uint32_t ri = static_cast<uint32_t>(ft * (16 * FT * rmul) + rowb[u]);  // row in the expert
+        const bool in = ft * (16 * FT) + fo[u] < nfeat;
+        ep[u] = ep[2 * WT + u] = 0u;
+        if constexpr (SM == kScaleChan) {
+          // two 16-bit halves (the upper one only for fp32 scales), so that
+          // the loads do not depend on the scale type
+          const __amdgpu_buffer_rsrc_t r = make_rsrc(static_cast<const uint8_t*>(lin ? p.sl : p.s) + e * rows * ses,
+                                                     static_cast<uint32_t>(rows * ses));
+          const uint32_t o = in ? ri * ses : kOob;
+          const uint32_t oh = in && ses == 4 ? ri * ses + 2 : kOob;
+          ep[u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(o), 0, 0));
+          ep[2 * WT + u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(oh), 0, 0));
         }
+        const void* bp = lin ? p.bl : p.b;
+        const __amdgpu_buffer_rsrc_t rb_ = make_rsrc(bp ? static_cast<const uint8_t*>(bp) + e * rows * 2 : nullptr,
+                                                     bp ? static_cast<uint32_t>(rows * 2) : 0u);
+        const uint32_t ob = in && (FC1 || s == 0) ? ri * 2 : kOob;
+        ep[WT + u] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(rb_, static_cast<int>(ob), 0, 0));
       }
+    };
+    auto ep_scale = [&](const uint32_t* ep, int u) -> float {
+      if constexpr (SM != kScaleChan) {
+        (void)ep;
+        (void)u;
+        return 1.0f;
+      } else {
+        const uint32_t r = ep[u];
+        if (ses == 4) return __uint_as_float(r | (ep[2 * WT + u] << 16));
+        if (p.scale_type == MOE_ELEM_FLOAT16) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+        return bf16_to_f32(static_cast<uint16_t>(r));
+      }
+    };
+    auto ep_bias = [&](uint32_t r) -> float {
+      if constexpr (AT::kId == 10) return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r)));
+      else return bf16_to_f32(static_cast<uint16_t>(r));
     };
 
     // scales, bias and activation of tile tl; store
-    auto finish = [&](int tl, const floatx4_t* v, const float* ep) {
+    auto finish = [&](int tl, const floatx4_t* v, const uint32_t* ep) {
       const int ft = f0 + tl;
       if constexpr (!FC1) {
 #pragma unroll
@@ -479,10 +560,11 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           const int f = ft * (16 * FT) + fo[u];
           if (f >= nfeat) continue;
           float* o = static_cast<float*>(p.out) + (static_cast<int64_t>(s) * p.out_rows + row0) * nfeat + f;
+          const float sc = ep_scale(ep, u), bi = ep_bias(ep[WT + u]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int m = 4 * g + r;
-            if (m < nrows) o[m * nfeat] = (v[u][r] - ctot[r]) * ep[u] + ep[WT + u];
+            if (m < nrows) o[m * nfeat] = (v[u][r] - ctot[r]) * sc + bi;
           }
         }
       } else {
@@ -492,12 +574,14 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           const int f = ft * (16 * FT) + fo[fi];
           if (f >= nfeat) continue;
           typename AT::storage* o = static_cast<typename AT::storage*>(p.out) + static_cast<int64_t>(row0) * nfeat + f;
+          const float sg = ep_scale(ep, ug), bg = ep_bias(ep[WT + ug]);
+          const float sl = ep_scale(ep, ul), bl = ep_bias(ep[WT + ul]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int m = 4 * g + r;
             if (m >= nrows) continue;
-            const float vg = (v[ug][r] - ctot[r]) * ep[ug] + ep[WT + ug];
-            const float vl = GATED ? (v[ul][r] - ctot[r]) * ep[ul] + ep[WT + ul] : 0.0f;
+            const float vg = (v[ug][r] - ctot[r]) * sg + bg;
+            const float vl = GATED ? (v[ul][r] - ctot[r]) * sl + bl : 0.0f;
             o[m * nfeat] = from_f32<AT>(apply_act<true>(vg, vl, GATED, p.activation, p.alpha, p.beta, p.limit));
           }
         }
@@ -506,26 +590,52 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
 
     // ---- this wave's run of blocks ----
     int lead_tl = -1, trail_tl = -1, seg0 = 0;
-    float ep[2 * WT];
+    uint32_t ep[3 * WT];
     int tl = b0 / bpt, cb = b0 - tl * bpt;
-    for (int b = b0; b < b1; ++b) {
-      if (cb == 0 || b == b0) {
+    // The waves of a SIMD compete for its issue slots, which go to the
+    // oldest wave among those of the highest priority.  With equal
+    // priorities the oldest wave races ahead and the youngest finishes its
+    // run long after, streaming alone; so each wave's priority follows the
+    // share of its run still ahead of it, and a wave that lags catches up.
+    const int run = b1 - b0;
+    auto set_prio = [&](int bj) {
+      const int rem = b1 - bj;
+      const int pr = rem * 4 > run * 3 ? 3 : (rem * 2 > run ? 2 : (rem * 4 > run ? 1 : 0));
+      if (pr == 3) __builtin_amdgcn_s_setprio(3);
+      else if (pr == 2) __builtin_amdgcn_s_setprio(2);
+      else if (pr == 1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    };
+    for (int bj = b0; bj < b1; ++bj) {
+      set_prio(bj);
+      if (cb == 0 || bj == b0) {
 #pragma unroll
         for (int u = 0; u < WT; ++u) acc[u] = floatx4_t{0.f, 0.f, 0.f, 0.f};
         seg0 = cb;
         load_ep(tl, ep);
       }
-      // next block of the run (past its end: loads that read nothing)
+      if constexpr (kTileScales) {
+        // chunk c = 4 cb + d of the slice: lane group c / 8 = cb / 2, dword
+        // (c % 8) / 2 = 2 (cb % 2) + d / 2, half d % 2
+        const int src = (col + 16 * (cb >> 1)) * 4;
+        const bool odd = cb & 1;
+#pragma unroll
+        for (int u = 0; u < WT; ++u) {
+          bsc[u][0] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(odd ? tsr[u][2] : tsr[u][0])));
+          bsc[u][1] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(odd ? tsr[u][3] : tsr[u][1])));
+        }
+      }
+      // the next block (past the run's end: loads that read nothing)
       const int ntl = cb + 1 == bpt ? tl + 1 : tl, ncb = cb + 1 == bpt ? 0 : cb + 1;
       uint32_t woff[WT], soff[WT];
       tile_offs(ntl, woff, soff);
-      if (b + 1 >= b1) {
+      if (bj + 1 >= b1) {
 #pragma unroll
         for (int u = 0; u < WT; ++u) woff[u] = soff[u] = kOob;
       }
       // chunks in groups of kStreamFetch: compute the group, then issue the
-      // loads of the same slots of the next block back to back (one row's
-      // consecutive 64-byte pieces reach the memory controller together)
+      // loads of the same slots back to back (one row's consecutive 64-byte
+      // pieces reach the memory controller together)
 #pragma unroll
       for (int h = 0; h < PD; h += kStreamFetch) {
 #pragma unroll
@@ -534,11 +644,15 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           // keep each chunk's LDS reads and dequantisation next to its MFMAs
           __builtin_amdgcn_sched_barrier(0);
         }
+        // the next tile's scales, once this block (the last of its tile) has
+        // read the current ones, ahead of the weights so that the next
+        // block's wait for them leaves the weights in flight
+        if (kTileScales && h + kStreamFetch == PD && cb == bpt - 1 && bj + 1 < b1) fetch_tsc(tl + 1);
 #pragma unroll
         for (int d = h; d < h + kStreamFetch; ++d) fetch(ncb * PD + d, woff, soff, ring[d]);
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (cb == bpt - 1 || b == b1 - 1) {
+      if (cb == bpt - 1 || bj == b1 - 1) {
         if (seg0 == 0 && cb == bpt - 1) {
           finish(tl, acc, ep);
         } else if (seg0 != 0) {
@@ -553,6 +667,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       cb = ncb;
     }
 
+    __builtin_amdgcn_s_setprio(0);
     // ---- split tiles: lead partials to LDS, owners add them in wave order ----
     __syncthreads();  // every wave is done with the activation slice
     if (lead_tl >= 0) {
