@@ -84,8 +84,6 @@ hipError_t dispatch_stream(const StreamStage& ss, const ExpertArgs& a, bool fc1,
 }  // namespace decode
 
 DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int wfmt, int gate_mode) {
-  (void)E;
-  (void)k;
   DecodePlan pl;
   if (T > kDecodeMaxTokens) return pl;
   pl.y2_planes_max = kMaxDecodeKsplit;
@@ -93,8 +91,12 @@ DecodePlan plan_decode(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, in
   // fc1 streams only when its whole K fits one LDS slice; fc2 always streams
   decode::stream_slices(H, decode::stream_pd(wfmt, gate_mode != kGateNone), &pl.nsl1, &pl.ksc1);
   decode::stream_slices(I, decode::stream_pd(wfmt, false), &pl.nsl2, &pl.ksc2);
-  pl.stream1 = pl.nsl1 == 1;
-  pl.stream2 = true;
+  // the stream kernel indexes its tiles (row groups x slices x feature
+  // tiles) with 32-bit arithmetic
+  const int64_t ng = decode::stream_groups(T, E, k);
+  const bool fits = ng * pl.nsl1 * ((I + 15) / 16) <= (int64_t{1} << 24) && ng * pl.nsl2 * ((H + 31) / 32) <= (int64_t{1} << 24);
+  pl.stream1 = pl.nsl1 == 1 && fits;
+  pl.stream2 = fits;
   pl.y2_planes_max = std::max<int32_t>(pl.nsl2, kMaxDecodeKsplit);
   return pl;
 }

@@ -240,10 +240,32 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   const int ktail = static_cast<int>(K - static_cast<int64_t>(nchunks - 1) * kChunk);
   const uint32_t rb = static_cast<uint32_t>((K / 32) * LB);  // bytes of one weight row
   const int nft = static_cast<int>((p.nfeat + 16 * FT - 1) / (16 * FT));
-  const int64_t per_a = static_cast<int64_t>(nsl) * nft;
-  const int64_t ttot = e_act * per_a;
-  const int64_t t_beg = ttot * blockIdx.x / gridDim.x;
-  const int64_t t_end = ttot * (blockIdx.x + 1) / gridDim.x;
+  // tile counts stay far below 2^31 (row groups x slices x feature tiles),
+  // so the partition and the group loop use 32-bit arithmetic
+  const int per_a = nsl * nft;
+  const int ttot = e_act * per_a;
+  // Tiles of group q (row group a = q / nsl, slice s = q % nsl) are
+  // [q nft, (q + 1) nft).  Each group a workgroup touches costs a staging
+  // and a split-tile reduction, about kGroupCost tiles of streaming.  With
+  // fewer groups than workgroups, each group gets a whole number of
+  // workgroups (group q: workgroups i with i G / P == q) when the largest
+  // share that leaves is cheaper than an even split of all tiles plus the
+  // second group that the workgroups on a group boundary then pay.
+  constexpr int kGroupCost = 2;
+  const int ngq = e_act * nsl, P = static_cast<int>(gridDim.x), bx = static_cast<int>(blockIdx.x);
+  int t_beg, t_end;
+  if (ngq <= P && (nft + P / ngq - 1) / (P / ngq) < kGroupCost + (ttot + P - 1) / P) {
+    const int q = bx * ngq / P;
+    const int w0 = (q * P + ngq - 1) / ngq, nw = ((q + 1) * P + ngq - 1) / ngq - w0;
+    const int j = bx - w0;
+    t_beg = q * nft + nft * j / nw;
+    t_end = q * nft + nft * (j + 1) / nw;
+  } else {
+    // floor(ttot * b / P) without a 64-bit product
+    const int qt = ttot / P, rt = ttot % P;
+    t_beg = qt * bx + rt * bx / P;
+    t_end = qt * (bx + 1) + rt * (bx + 1) / P;
+  }
   const int bpt = ksc / PD;  // blocks per tile
   int bshift = 0;
   uint32_t nblk = 0;
@@ -281,11 +303,11 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     asm volatile("" : "+v"(m_hi));
   }
 
-  for (int64_t t = t_beg; t < t_end;) {
-    const int a = static_cast<int>(t / per_a);
-    const int rem = static_cast<int>(t - a * per_a);
+  for (int t = t_beg; t < t_end;) {
+    const int a = t / per_a;
+    const int rem = t - a * per_a;
     const int s = rem / nft, f0 = rem - s * nft;
-    const int ntl = static_cast<int>(t_end - t < nft - f0 ? t_end - t : nft - f0);
+    const int ntl = t_end - t < nft - f0 ? t_end - t : nft - f0;
     const int nb = ntl * bpt;
     const int b0 = nb * wave / NW, b1 = nb * (wave + 1) / NW;
     const int ent = __builtin_amdgcn_readfirstlane(exl[a]);
@@ -366,7 +388,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int gpr = ksc / 4;        // 1 KB groups per row
     const int ngr = nrows * gpr;    // groups of the slice
     // source row of row m (fc1: the token of dispatched row row0 + m), lane m
-    const int srcl = FC1 ? (lane < nrows ? static_cast<int>(p.perm[row0 + lane] / p.topk) : 0) : row0 + lane;
+    const int srcl = FC1 ? (lane < nrows ? p.perm[row0 + lane] / static_cast<int>(p.topk) : 0) : row0 + lane;
     for (int q = wave; q < ngr; q += NW) {
       const int m = q / gpr, r = (q - m * gpr) * 64 + lane;  // row, piece in the row
       const int64_t k = static_cast<int64_t>(cs0 + (r >> 4)) * kChunk + (r & 15) * 8;
