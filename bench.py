@@ -88,7 +88,7 @@ def measured_traffic(key: str):
     return ent["bytes"] if ent else None
 
 
-def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=False):
+def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=False, prepack=True):
     import torch
 
     from onnxruntime_musa_amd.workloads import CONFIGS, make_problem
@@ -97,6 +97,10 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
     prob = make_problem(cfg, T, seed=1234, device=dev)
     op = prob.make_op()
     inputs = prob.schema_inputs()
+    # session set-up: QMoE expert weights pre-packed once (not timed), as a
+    # plugin EP's PrePack does for constant initializers
+    packed = op.prepack_all(*inputs) if prepack else []
+    torch.cuda.synchronize()
     ws = torch.empty((op.workspace_size(*inputs),), dtype=torch.uint8, device=dev)
     out = torch.empty_like(inputs[0])
     call = op.bind(*inputs, out=out, workspace=ws)
@@ -137,7 +141,7 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
         roof = dict(bound="mfma", achieved=round(fc1_ach, 1), peak=PEAK_MFMA_TFLOPS, unit="TFLOP/s",
                     frac=round(fc1_ach / PEAK_MFMA_TFLOPS, 4), traffic=traffic)
     layer_s = ms_per_step * 1e-3
-    res = dict(workload=name, tokens=T, path=path, ms_per_step=round(ms_per_step, 4),
+    res = dict(workload=name, tokens=T, path=path, prepacked=packed, ms_per_step=round(ms_per_step, 4),
                tokens_per_s=round(T / layer_s, 1), experts_hit=hit,
                layer_hbm_gbs=round(cost["layer_bytes"] / layer_s / 1e9, 1),
                layer_tflops=round(cost["layer_flops"] / layer_s / 1e12, 2),
@@ -183,6 +187,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default=None, help="name:tokens to run instead of the headline")
+    ap.add_argument("--no-prepack", action="store_true", help="keep the expert weights in the op's row-major layout")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -208,7 +213,8 @@ def main():
     if args.workload:
         name, t = args.workload.split(":")
         T = int(t)
-    head, prob = run_workload(name, T, args.steps, args.warmup, dev, keep_problem=True)
+    head, prob = run_workload(name, T, args.steps, args.warmup, dev, keep_problem=True,
+                              prepack=not args.no_prepack)
     print(f"[bench] {name} T={T}: {head['tokens_per_s']} tok/s, {head['ms_per_step']} ms, "
           f"fc1 {head['roofline']['achieved']} {head['roofline']['unit']}", file=sys.stderr, flush=True)
     cpu = None
@@ -220,7 +226,8 @@ def main():
     extra = []
     if not args.no_extra and not args.workload:
         for wname, wT in EXTRA:
-            r, _ = run_workload(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev)
+            r, _ = run_workload(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev,
+                                prepack=not args.no_prepack)
             extra.append(r)
             print(f"[bench] {wname} T={wT}: {r['tokens_per_s']} tok/s, {r['ms_per_step']} ms, path={r['path']}, "
                   f"fc1 {r['roofline']['achieved']} {r['roofline']['unit']} ({r['roofline']['frac']:.1%})",
@@ -244,7 +251,8 @@ def main():
                    "experts": cfg.experts, "k": cfg.k,
                    "weights": (f"int{cfg.bits} " + (f"block {cfg.block_size}" if cfg.block_size else "per-channel")
                                + f", {cfg.scale_dtype} scales") if cfg.bits else cfg.dtype,
-                   "path": head["path"], "experts_hit": head["experts_hit"]},
+                   "path": head["path"], "experts_hit": head["experts_hit"],
+                   "prepacked_inputs": head["prepacked"]},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
         "stages_ms": head["stages_ms"],

@@ -155,6 +155,37 @@ MOE_API moe_status moe_kernel_workspace_layout(const moe_kernel *kernel, const m
  * Call before the kernel is shared between threads. */
 MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
 
+/* Weight pre-pack at session initialisation: the role of ONNX Runtime's
+ * OpKernel::PrePack(tensor, input_idx, alloc, is_packed, prepacked_weights)
+ * (onnxruntime/core/framework/op_kernel.h of ORT 1.26, not vendored in the
+ * reference; the reference carries the session option that shares pre-packed
+ * weights, "ep.musa.enable_prepack_weight_sharing",
+ * musa/ep/src/ep_factory.cc:472-478, musa/ep/src/ep.h:35).
+ *
+ * QMoE expert weights (input_index 2 fc1, 5 fc2, 8 fc3; `weights` is the
+ * constant initializer on the device) are reordered once into a tile-major
+ * layout: each 16 rows x 128 k of an expert's [N, K/pack] matrix become one
+ * contiguous block (1 KB int4, 2 KB int8), so that every load instruction
+ * of the decode kernels reads one 1 KB run.  act_type is the op's input
+ * element type T (known from the node at kernel creation).
+ *
+ * moe_kernel_prepack_size: bytes of the packed copy, or 0 when the kernel
+ *   reads that input in the op's layout (MoE, fp32 activations, N not a
+ *   multiple of 16, K not a multiple of 128, interleaved SwiGLU fc1, fc1/fc3
+ *   K above 4096).
+ * moe_kernel_prepack: writes the packed copy into dst (device, at least that
+ *   many bytes, 16-byte aligned) on stream, records dst and sets *is_packed.
+ *   Every later compute (and workspace query) reads that input from dst; the
+ *   caller may then pass data == NULL for it (its shape is taken from the
+ *   packed tensor) or the same tensor (shape checked).  dst must stay valid
+ *   while the kernel lives; the source may be freed once the stream has run
+ *   the pack.  fc1 and fc3 are packed together or not at all.  Call before
+ *   the kernel is shared between threads. */
+MOE_API moe_status moe_kernel_prepack_size(const moe_kernel *kernel, int32_t input_index,
+                                           const moe_tensor *weights, int32_t act_type, size_t *bytes);
+MOE_API moe_status moe_kernel_prepack(moe_kernel *kernel, int32_t input_index, const moe_tensor *weights,
+                                      int32_t act_type, void *dst, size_t dst_bytes, void *stream,
+                                      int32_t *is_packed);
 /* Stage profiling (the role of the reference's EP profiler hooks,
  * musa/ep/src/ep_profiling.cc:141-288, with real producers): when enabled,
  * moe_kernel_compute records HIP events on its stream around each stage.

@@ -66,6 +66,7 @@ struct Stage {
   int32_t gate_mode, scale_type, activation, ks;
   int32_t ksg;        // K splits across workgroups (fc2 only)
   int32_t lds_scale;  // bytes of LDS per wave for staged scales
+  int32_t tiled;      // weights tile-major (stream kernel only)
   int64_t block_size;
   float alpha, beta, limit;
   const int32_t* offsets;

@@ -151,6 +151,7 @@ decode::Stage fc1_stage(const ExpertArgs& a) {
   st.topk = a.k;
   st.out = a.act;
   st.out_rows = a.T * a.k;
+  st.tiled = a.tiled1;
   return st;
 }
 
@@ -177,6 +178,7 @@ decode::Stage fc2_stage(const ExpertArgs& a) {
   st.topk = a.k;
   st.out = a.y2;
   st.out_rows = a.T * a.k;
+  st.tiled = a.tiled2;
   return st;
 }
 

@@ -89,6 +89,7 @@ struct PStage {
   int32_t ksplit;   // K splits (partial planes of the output)
   int32_t out_half; // fc2 with one plane: y2 stored in the activation type
   int32_t kstages;  // stages per K split
+  int32_t tiled;    // weights tile-major (int4 / int8)
   int64_t out_rows;
   void* out;  // fc1: act [rows, nfeat] (AT); fc2: y2 [ksplit][rows, nfeat] fp32
 };
@@ -164,7 +165,23 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
     drow[0] = 0;
     drow[1] = 32;
   }
-  const uint32_t woff = static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
+  // Tile-major weights (pre-packed, int4 / int8; a stage is one chunk of
+  // 128 k): the 16 rows x 128 k of a weight tile and chunk are one block of
+  // CB bytes in which piece q (16 bytes) of row r sits at ((q % kv) * 64 + (q
+  // / kv) * 16 + r) * 16, kv = 16-byte vectors per 32 k.  Lane half h reads
+  // pieces BVEC h .. BVEC h + BVEC - 1 of its row.  drow steps (0, 32, nfeat)
+  // are whole tiles, so they stay row offsets.
+  constexpr int kKv = WF == kInt8 ? 2 : 1;
+  constexpr int CB = 1024 * kKv;
+  const bool tiled = WF != kDense && p.tiled != 0;
+  const uint32_t woff =
+      tiled ? static_cast<uint32_t>((row0 / 16) * 16 * rb + (row0 % 16) * 16 + static_cast<int64_t>(kbeg / BK) * CB + 512 * h)
+            : static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
+  const int cstride = tiled ? CB : BK * G::EBITS / 8;  // weight bytes per stage
+  // offset of vector v beyond 16 v (tiled: piece BVEC h + v)
+  int vdelta[BVEC];
+#pragma unroll
+  for (int v = 0; v < BVEC; ++v) vdelta[v] = tiled ? (v % kKv) * 1024 + (v / kKv) * 256 - 16 * v : 0;
 
   // ---- per-block scales (folded).  Loading a 2-byte scale per lane and
   // stage touches one cache line per row, as much address work as a weight
@@ -226,7 +243,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   auto fetch = [&](int c, Ring& d) {
     const int k0 = kbeg + c * BK + KH * h;  // first k of the lane's range
     const bool kin = (c < nst) & (k0 < K);
-    const uint32_t o = kin ? woff + static_cast<uint32_t>(c * BK * G::EBITS / 8) : kOob;
+    const uint32_t o = kin ? woff + static_cast<uint32_t>(c * cstride) : kOob;
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
       const __amdgpu_buffer_rsrc_t rw = GATED && j == 1 ? rs_l : rs_g;
@@ -234,7 +251,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 #pragma unroll
       for (int v = 0; v < BVEC; ++v)
         d.w[j][v] = __builtin_bit_cast(
-            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw, 0));
+            u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, static_cast<int>(o + 16 * v), sw + vdelta[v], 0));
     }
   };
 
@@ -589,6 +606,7 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream) {
   st.topk = a.k;
   st.out_rows = a.T * a.k;
   st.out = a.act;
+  st.tiled = a.tiled1;
   // gated: a weight tile holds BN/2 features (gate + linear rows)
   plan_grid(st, a.T, a.k, a.E, a.wfmt, gated ? 2 * a.I : a.I, 1);
   return launch_stage<true>(st, a, gated, stream);
@@ -619,6 +637,7 @@ hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half,
   st.topk = a.k;
   st.out_rows = a.T * a.k;
   st.out = a.y2;
+  st.tiled = a.tiled2;
   const int32_t splits = prefill_fc2_splits(a.T, a.H, a.I, a.E, a.k, a.wfmt);
   plan_grid(st, a.T, a.k, a.E, a.wfmt, a.H, splits);
   // fp16 and one plane: y2 goes out in fp16 (one rounding of the expert

@@ -56,6 +56,7 @@ namespace decode {
 constexpr int kStreamRows = 16;       // token rows staged (the MFMA M dimension)
 constexpr int kStreamMaxChunks = 32;  // K chunks of one staged slice (16 x 32 x 256 B of LDS)
 constexpr int kStreamFetch = 4;       // chunks whose loads are issued back to back
+static_assert(kStreamMaxChunks * kChunk == kStreamMaxK, "host and kernel agree on the slice size");
 
 // Chunks per block; a K slice is a whole number of blocks.
 inline int stream_pd(int wfmt, bool gated) {
@@ -282,6 +283,14 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // row's byte offsets with the tile index factored out (32-bit: one
   // expert's weights are below 2 GiB).
   const int rmul = (FC1 && GATED && p.gate_mode == kGateInterleaved) ? 2 : 1;
+  // Tile-major weights (pre-packed; weight tiles start at a multiple of 16
+  // rows, K is whole chunks): the 16 rows x 128 k of a weight tile and chunk
+  // are one contiguous block, lane l's 16 bytes at 16 l (vector v of int8
+  // one 1 KB block further), so that each load instruction reads 1 KB in
+  // one run.  Row-major: row col, bytes [LB g, LB g + LB) of the chunk.
+  const bool tiled = p.tiled != 0;
+  const uint32_t cstride = tiled ? 64 * LB : 4 * LB;  // weight bytes per chunk
+  const int vdelta = tiled ? 1024 - 16 : 0;           // extra offset of vector v, per v
   int fo[WT], rowb[WT];
   uint32_t wb[WT], sb[WT];
 #pragma unroll
@@ -290,7 +299,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int radd = !lin ? 0 : (p.gate_mode == kGateInterleaved ? 1 : (p.gate_mode == kGateChunked ? nfeat : 0));
     fo[u] = (u % FT) * 16 + col;
     rowb[u] = fo[u] * rmul + radd;
-    wb[u] = static_cast<uint32_t>(rowb[u]) * rb + g * LB;
+    wb[u] = tiled ? static_cast<uint32_t>(rowb[u] - col) * rb + lane * 16 : static_cast<uint32_t>(rowb[u]) * rb + g * LB;
     sb[u] = static_cast<uint32_t>(rowb[u]) * nblk * kEs;
   }
   const uint32_t tws = static_cast<uint32_t>(16 * FT * rmul) * rb;          // weight bytes per tile step
@@ -361,12 +370,15 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       // read nothing (branch-free: one compare against the chunk's valid k)
       const int kval = cg < nchunks - 1 ? kChunk : (cg == nchunks - 1 ? ktail : 0);
       const uint32_t oob = 32 * g + 32 <= kval ? 0u : kOob;
-      const uint32_t wc = static_cast<uint32_t>(cg) * (4 * LB);
+      const uint32_t wc = static_cast<uint32_t>(cg) * cstride;
 #pragma unroll
       for (int u = 0; u < WT; ++u) {
         const uint32_t o = (woff[u] + wc) | oob;
 #pragma unroll
-        for (int v = 0; v < G::kVecs; ++v) d.w[u][v] = bload16(GATED && u >= FT ? rs_l : rs_g, o + 16 * v);
+        for (int v = 0; v < G::kVecs; ++v)
+          d.w[u][v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      GATED && u >= FT ? rs_l : rs_g, static_cast<int>(o + 16 * v),
+                                                      v * vdelta, 0));
         if constexpr (kRingScales && !kTileScales) {
           const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (SM == kScaleFold ? 32 * g : 0);
           // a block scale multiplies the whole chunk's sum (every lane group

@@ -61,6 +61,9 @@ struct ExpertArgs {
   const void *w3, *s3, *b3;
   // fc2
   const void *w2, *s2, *b2;
+  // 1: the stage's weights are in the tile-major layout of moe_prepack.hip
+  // (fc1 and fc3 together; fc2), else in the op's row-major layout
+  int32_t tiled1, tiled2;
   // intermediates
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
@@ -77,6 +80,12 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half, hipStream_t stream);
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
 
+// Reorders row-major quantized weights [rows, row_bytes] (rows a multiple of
+// 16, row_bytes a multiple of the chunk row bytes cbytes = 64 for int4, 128
+// for int8) into the tile-major layout read by the decode and prefill kernels.
+hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
+                          hipStream_t stream);
+
 // Whether the MFMA paths accept this problem (fp16/bf16 activations, K a
 // multiple of 32, block sizes the dequant loaders handle).
 bool decode_supported(const ExpertArgs& a);
@@ -91,6 +100,9 @@ constexpr int64_t kDecodeMaxTokens = 64;
 // Token count up to which decode stages the activation rows in LDS (in
 // groups of 16 rows per expert).
 constexpr int64_t kLdsMaxTokens = 64;
+// Largest K of one LDS activation slice of the decode stream kernel (32
+// chunks of 128 k); fc1 streams only when its K fits one slice.
+constexpr int64_t kStreamMaxK = 32 * 128;
 // Most K splits across workgroups of the decode fc2 kernel (partial planes of y2).
 constexpr int kMaxDecodeKsplit = 8;
 

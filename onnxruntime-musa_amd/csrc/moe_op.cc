@@ -111,6 +111,14 @@ struct moe_kernel {
   hipEvent_t ev[5] = {};
   bool ev_recorded = false;
   int32_t last_path = -1;
+  // Pre-packed (tile-major) expert weights by QMoE input index (2 fc1, 5
+  // fc2, 8 fc3): the caller-owned device copy and the tensor it was packed
+  // from (shape and type; its data pointer is not kept).
+  struct Packed {
+    const void* data = nullptr;
+    moe_tensor src{};
+  };
+  Packed packed[11];
 
   ~moe_kernel() {
     for (auto& kv : ws_cache)
@@ -260,6 +268,61 @@ moe_status validate(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, P
   return MOE_OK;
 }
 
+// Inputs of one call with pre-packed weights in place of theirs: a packed
+// input may come with data == NULL (shape taken from the packed tensor) or
+// with a descriptor that must match the tensor that was packed.
+moe_status with_packed(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, moe_tensor* local) {
+  for (int32_t i = 0; i < n; ++i) local[i] = inputs[i];
+  for (int32_t i = 0; i < n && i < 11; ++i) {
+    const auto& pk = kr->packed[i];
+    if (!pk.data) continue;
+    if (inputs[i].data) {
+      bool same = inputs[i].elem_type == pk.src.elem_type && inputs[i].rank == pk.src.rank;
+      for (int d = 0; same && d < pk.src.rank; ++d) same = inputs[i].dims[d] == pk.src.dims[d];
+      if (!same)
+        return fail(MOE_INVALID_ARGUMENT, "input " + std::to_string(i) + " " + dims_str(inputs[i]) +
+                                              " differs from the pre-packed weights " + dims_str(pk.src));
+    } else {
+      local[i] = pk.src;
+    }
+    local[i].data = pk.data;
+  }
+  return MOE_OK;
+}
+
+// Bytes of the tile-major copy of QMoE weight input idx, or 0 when the
+// kernels read that input in the op's layout (see moe_prepack.hip).  A
+// weight is packed when each expert's rows are whole 16-row tiles and K is
+// whole chunks of 128, and the kernels that read it take tile-major weights:
+// fp16/bf16 activations (MFMA paths); fc1/fc3 with K within one decode
+// activation slice and gate/linear rows in separate tiles (not interleaved).
+moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w, int32_t act_type,
+                         size_t* bytes) {
+  *bytes = 0;
+  if (idx != 2 && idx != 5 && idx != 8)
+    return fail(MOE_INVALID_ARGUMENT, "input_index must be 2, 5 or 8 (QMoE expert weights), got " +
+                                          std::to_string(idx));
+  if (!w || !w->data) return fail(MOE_INVALID_ARGUMENT, "null weights");
+  if (!is_float_type(act_type)) return fail(MOE_INVALID_ARGUMENT, "act_type must be a float type");
+  if (!kr->quantized) return MOE_OK;
+  if (w->elem_type != MOE_ELEM_UINT8 || w->rank != 3 || w->dims[0] <= 0)
+    return fail(MOE_INVALID_ARGUMENT, "QMoE expert weights must be 3D uint8, got " + dims_str(*w));
+  if (act_type == MOE_ELEM_FLOAT) return MOE_OK;
+  const moe_attributes& at = kr->attrs;
+  const int64_t cbytes = at.expert_weight_bits == 4 ? 64 : 128;
+  const int64_t E = w->dims[0], N = w->dims[1], rb = w->dims[2];
+  const bool swiglu = at.activation_type == MOE_ACT_SWIGLU;
+  if (N <= 0 || N % 16 || rb <= 0 || rb % cbytes) return MOE_OK;
+  if (N * rb >= (int64_t{1} << 31)) return MOE_OK;  // 32-bit buffer offsets per expert
+  if (idx != 5) {
+    if (rb / cbytes * 128 > moe::kStreamMaxK) return MOE_OK;
+    if (swiglu && at.swiglu_fusion == 1) return MOE_OK;
+    if (swiglu && at.swiglu_fusion == 2 && N % 32) return MOE_OK;
+  }
+  *bytes = static_cast<size_t>(E * N * rb);
+  return MOE_OK;
+}
+
 moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout& l, uint8_t* ws,
                             void* output) {
   const bool q = kr->quantized;
@@ -289,6 +352,8 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   } else {
     a.b1 = d(3); a.w2 = d(4); a.b2 = d(5); a.w3 = d(6); a.b3 = d(7);
   }
+  a.tiled1 = q && kr->packed[2].data ? 1 : 0;
+  a.tiled2 = q && kr->packed[5].data ? 1 : 0;
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
   a.y2_planes = 1;
@@ -297,15 +362,23 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   return a;
 }
 
+// Expert-kernel family of a call, -1 when none takes it.  Tile-major
+// weights are read by the decode stream kernels and the prefill kernels only.
 int choose_path(const moe_kernel* kr, const moe::ExpertArgs& a) {
   const int forced = kr->forced_path;
-  if (forced == moe::kPathSimt) return moe::kPathSimt;
-  if (forced == moe::kPathDecode && moe::decode_supported(a)) return moe::kPathDecode;
-  if (forced == moe::kPathPrefill && moe::prefill_supported(a)) return moe::kPathPrefill;
-  if (forced >= 0) return -1;
-  if (moe::decode_supported(a)) return moe::kPathDecode;
-  if (moe::prefill_supported(a)) return moe::kPathPrefill;
-  return moe::kPathSimt;
+  const bool tiled = a.tiled1 || a.tiled2;
+  bool decode = moe::decode_supported(a);
+  if (decode && tiled) {
+    const moe::DecodePlan pl = moe::plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
+    decode = (!a.tiled1 || pl.stream1) && (!a.tiled2 || pl.stream2);
+  }
+  const bool prefill = moe::prefill_supported(a);
+  if (forced == moe::kPathSimt) return tiled ? -1 : moe::kPathSimt;
+  if (forced == moe::kPathDecode) return decode ? moe::kPathDecode : -1;
+  if (forced == moe::kPathPrefill) return prefill ? moe::kPathPrefill : -1;
+  if (decode) return moe::kPathDecode;
+  if (prefill) return moe::kPathPrefill;
+  return tiled ? -1 : moe::kPathSimt;
 }
 
 moe_status hip_fail(hipError_t e, const char* what) {
@@ -387,12 +460,54 @@ moe_status moe_kernel_set_expert_path(moe_kernel* kernel, int32_t path) {
   return MOE_OK;
 }
 
+moe_status moe_kernel_prepack_size(const moe_kernel* kernel, int32_t input_index, const moe_tensor* weights,
+                                   int32_t act_type, size_t* bytes) {
+  try {
+    if (!kernel || !bytes) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    return prepack_bytes(kernel, input_index, weights, act_type, bytes);
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
+moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe_tensor* weights, int32_t act_type,
+                              void* dst, size_t dst_bytes, void* stream, int32_t* is_packed) {
+  try {
+    if (!kernel || !is_packed) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    *is_packed = 0;
+    size_t need = 0;
+    const moe_status st = prepack_bytes(kernel, input_index, weights, act_type, &need);
+    if (st != MOE_OK) return st;
+    if (need == 0) return MOE_OK;
+    if (!dst || dst_bytes < need)
+      return fail(MOE_INVALID_ARGUMENT, "pre-pack buffer too small: need " + std::to_string(need) + " bytes");
+    if (reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(weights->data) % 16)
+      return fail(MOE_INVALID_ARGUMENT, "weights and pre-pack buffer must be 16-byte aligned");
+    const int cbytes = kernel->attrs.expert_weight_bits == 4 ? 64 : 128;
+    const hipError_t e = moe::launch_prepack(static_cast<const uint8_t*>(weights->data), static_cast<uint8_t*>(dst),
+                                             weights->dims[0] * weights->dims[1], weights->dims[2], cbytes,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "pre-pack launch");
+    kernel->packed[input_index].data = dst;
+    kernel->packed[input_index].src = *weights;
+    kernel->packed[input_index].src.data = nullptr;
+    *is_packed = 1;
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
 moe_status moe_kernel_workspace_size(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n,
                                      size_t* bytes) {
   try {
     if (!kernel || !bytes) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    if (!inputs || n < 0 || n > 64) return fail(MOE_INVALID_ARGUMENT, "bad inputs");
+    moe_tensor local[64];
+    moe_status st = with_packed(kernel, inputs, n, local);
+    if (st != MOE_OK) return st;
     Problem p;
-    const moe_status st = validate(kernel, inputs, n, &p);
+    st = validate(kernel, local, n, &p);
     if (st != MOE_OK) return st;
     *bytes = plan_layout(p).total;
     return MOE_OK;
@@ -405,8 +520,12 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
                                        moe_workspace_layout* out) {
   try {
     if (!kernel || !out) return fail(MOE_INVALID_ARGUMENT, "null argument");
+    if (!inputs || n < 0 || n > 64) return fail(MOE_INVALID_ARGUMENT, "bad inputs");
+    moe_tensor local[64];
+    moe_status st = with_packed(kernel, inputs, n, local);
+    if (st != MOE_OK) return st;
     Problem p;
-    const moe_status st = validate(kernel, inputs, n, &p);
+    st = validate(kernel, local, n, &p);
     if (st != MOE_OK) return st;
     const Layout l = plan_layout(p);
     out->topk_ids = l.topk_ids;
@@ -428,8 +547,12 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
                               void* workspace, size_t workspace_bytes, void* stream_ptr) {
   try {
     if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+    if (!inputs || n < 0 || n > 64) return fail(MOE_INVALID_ARGUMENT, "bad inputs");
+    moe_tensor local[64];
+    moe_status st = with_packed(kernel, inputs, n, local);
+    if (st != MOE_OK) return st;
     Problem p;
-    moe_status st = validate(kernel, inputs, n, &p);
+    st = validate(kernel, local, n, &p);
     if (st != MOE_OK) return st;
     if (p.T == 0) return MOE_OK;
     if (!output) return fail(MOE_INVALID_ARGUMENT, "null output");
@@ -480,8 +603,13 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     ra.tile_offsets = reinterpret_cast<int32_t*>(ws + l.tile_offsets);
     ra.tile_m = moe::kPrefillTileM;
     moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
+    if (p.gate_mode == moe::kGateFc3 && (kernel->packed[2].data != nullptr) != (kernel->packed[8].data != nullptr))
+      return fail(MOE_NOT_IMPLEMENTED, "fc1 and fc3 weights must both be pre-packed or neither");
     const int path = choose_path(kernel, a);
-    if (path < 0) return fail(MOE_NOT_IMPLEMENTED, "forced expert path does not support this problem");
+    if (path < 0)
+      return fail(MOE_NOT_IMPLEMENTED, kernel->forced_path >= 0
+                                           ? "forced expert path does not support this problem"
+                                           : "pre-packed weights need fp16/bf16 activations (MFMA kernels)");
 
     auto* mk = const_cast<moe_kernel*>(kernel);
     const bool prof = mk->profiling;

@@ -89,6 +89,11 @@ EXPORTS = [
     ("moe_kernel_workspace_layout", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                                    ctypes.POINTER(MoeWorkspaceLayout)]),
     ("moe_kernel_set_expert_path", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    ("moe_kernel_prepack_size", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(MoeTensor),
+                                               ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    ("moe_kernel_prepack", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(MoeTensor), ctypes.c_int32,
+                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                          ctypes.POINTER(ctypes.c_int32)]),
     ("moe_kernel_set_profiling", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
     ("moe_kernel_stage_times", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_float),
                                               ctypes.POINTER(ctypes.c_int32)]),

@@ -83,6 +83,7 @@ class _MoEOp:
         check(lib.moe_kernel_create(self.op_type.encode(), ctypes.byref(a), ctypes.byref(h)))
         self._h = h
         self.attributes = a
+        self._packed = {}
         if expert_path != "auto":
             check(lib.moe_kernel_set_expert_path(h, PATHS[expert_path]))
 
@@ -91,6 +92,42 @@ class _MoEOp:
         if h is not None and h.value:
             self._lib.moe_kernel_release(h)
             self._h = None
+
+    WEIGHT_INPUTS = ()
+
+    def prepack(self, input_index: int, weights: torch.Tensor, act_dtype: torch.dtype,
+                stream: Optional[torch.cuda.Stream] = None) -> Optional[torch.Tensor]:
+        """Pre-packs one expert-weight input at session set-up: the role of
+        ONNX Runtime's OpKernel::PrePack for a constant initializer.  Returns
+        the tile-major device copy, which every later call reads in place of
+        that input (the op keeps it alive), or None when the kernel reads that
+        input in the op's layout."""
+        d = _tensor_desc(weights)
+        nb = ctypes.c_size_t()
+        check(self._lib.moe_kernel_prepack_size(self._h, int(input_index), ctypes.byref(d), _ELEM[act_dtype],
+                                                ctypes.byref(nb)))
+        if nb.value == 0:
+            return None
+        dst = torch.empty((nb.value,), dtype=torch.uint8, device=weights.device)
+        s = stream if stream is not None else torch.cuda.current_stream(weights.device)
+        packed = ctypes.c_int32()
+        check(self._lib.moe_kernel_prepack(self._h, int(input_index), ctypes.byref(d), _ELEM[act_dtype],
+                                           ctypes.c_void_p(dst.data_ptr()), nb.value, ctypes.c_void_p(s.cuda_stream),
+                                           ctypes.byref(packed)))
+        if not packed.value:
+            return None
+        self._packed[int(input_index)] = dst
+        return dst
+
+    def prepack_all(self, *inputs) -> list:
+        """Pre-packs every expert-weight input present in a schema-ordered
+        input list; returns the input indices that were packed."""
+        done = []
+        act = inputs[0].dtype
+        for i in self.WEIGHT_INPUTS:
+            if i < len(inputs) and inputs[i] is not None and self.prepack(i, inputs[i], act) is not None:
+                done.append(i)
+        return done
 
     def _descs(self, inputs):
         if len(inputs) > len(self.input_names):
@@ -170,6 +207,7 @@ class QMoE(_MoEOp):
     """com.microsoft QMoE (int8 / int4 expert weights with scales)."""
     op_type = "QMoE"
     input_names = QMOE_INPUTS
+    WEIGHT_INPUTS = (2, 5, 8)  # fc1, fc2, fc3 expert weights
 
 
 def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoid: bool = False,

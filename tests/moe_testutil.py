@@ -29,9 +29,11 @@ def compare_outputs(got: np.ndarray, exp: np.ndarray, dtype: str, what: str, row
     return float(np.max(np.abs(g - e))) if g.size else 0.0
 
 
-def run_op(problem: Problem, path: str = "auto", with_workspace: bool = False):
+def run_op(problem: Problem, path: str = "auto", with_workspace: bool = False, prepack: bool = False):
     op = problem.make_op(expert_path=path)
     inputs = problem.schema_inputs()
+    if prepack:
+        assert op.prepack_all(*inputs), "no expert weight was pre-packed"
     ws = None
     layout = None
     if with_workspace:
@@ -55,11 +57,11 @@ def run_op(problem: Problem, path: str = "auto", with_workspace: bool = False):
     return y, routing
 
 
-def check_problem(problem: Problem, path: str = "auto", sample_tokens=None, seed=0, threads=0):
+def check_problem(problem: Problem, path: str = "auto", sample_tokens=None, seed=0, threads=0, prepack=False):
     """Runs the HIP op and the oracle on the same inputs and compares.
     sample_tokens: compute the oracle's expert FFN for this many sampled tokens
     only (routing is still checked for every token)."""
-    y, routing = run_op(problem, path, with_workspace=True)
+    y, routing = run_op(problem, path, with_workspace=True, prepack=prepack)
     host = {n: to_host(t) for n, t in problem.inputs.items()}
     T = problem.tokens
     mask, rows = None, None

@@ -266,3 +266,94 @@ def test_set_expert_path_validates(lib, qkernel):
     assert lib.moe_kernel_set_expert_path(qkernel, 1) == C.MOE_OK
     assert lib.moe_kernel_set_expert_path(qkernel, 7) == C.MOE_INVALID_ARGUMENT
     assert lib.moe_kernel_set_expert_path(qkernel, -1) == C.MOE_OK
+
+
+# ---- weight pre-pack (the OpKernel::PrePack role): which inputs a kernel
+# packs, and how many bytes the tile-major copy takes.  prepack_size reads
+# the shape and type only. ----
+def prepack_size(lib, h, idx, dims, act=C.ELEM_FLOAT16, et=C.ELEM_UINT8):
+    t = tensor(dims, et)
+    n = ctypes.c_size_t(123)
+    st = lib.moe_kernel_prepack_size(h, idx, ctypes.byref(t), act, ctypes.byref(n))
+    return st, n.value
+
+
+@pytest.mark.parametrize("bits,idx,dims,packed", [
+    (4, 2, [8, 512, 128], True),     # fc1 int4: H = 256 -> whole chunks, 16-row tiles
+    (4, 5, [8, 256, 256], True),     # fc2 int4, I = 512
+    (4, 8, [8, 512, 128], True),     # fc3
+    (8, 2, [8, 512, 256], True),     # int8
+    (4, 2, [8, 520, 128], False),    # N not a multiple of 16
+    (4, 2, [8, 512, 96], False),     # K = 192: not whole chunks of 128
+    (8, 5, [8, 256, 192], False),    # int8 K = 192
+    (4, 2, [8, 512, 4096], False),   # fc1 K = 8192: above one decode activation slice
+    (4, 5, [8, 512, 4096], True),    # fc2 K = 8192 streams in slices
+])
+def test_prepack_size_rules(lib, bits, idx, dims, packed):
+    st, h = create(lib, "QMoE", k=2, activation_type=4, block_size=128, expert_weight_bits=bits)
+    assert st == C.MOE_OK
+    try:
+        st, n = prepack_size(lib, h, idx, dims)
+        assert st == C.MOE_OK, lib.moe_last_error()
+        assert n == (dims[0] * dims[1] * dims[2] if packed else 0)
+    finally:
+        lib.moe_kernel_release(h)
+
+
+def test_prepack_size_interleaved_fc1_stays_row_major(lib):
+    st, h = create(lib, "QMoE", k=2, activation_type=4, swiglu_fusion=1, block_size=32)
+    assert st == C.MOE_OK
+    try:
+        assert prepack_size(lib, h, 2, [8, 1024, 128]) == (C.MOE_OK, 0)
+        assert prepack_size(lib, h, 5, [8, 256, 256])[1] == 8 * 256 * 256
+    finally:
+        lib.moe_kernel_release(h)
+
+
+def test_prepack_size_chunked_fc1_needs_whole_tiles_per_half(lib):
+    st, h = create(lib, "QMoE", k=2, activation_type=4, swiglu_fusion=2, block_size=0)
+    assert st == C.MOE_OK
+    try:
+        assert prepack_size(lib, h, 2, [8, 1024, 128])[1] == 8 * 1024 * 128
+        assert prepack_size(lib, h, 2, [8, 48, 128]) == (C.MOE_OK, 0)  # I = 24: the linear half starts mid-tile
+    finally:
+        lib.moe_kernel_release(h)
+
+
+def test_prepack_size_fp32_activations_and_moe_stay_row_major(lib, qkernel):
+    assert prepack_size(lib, qkernel, 2, [8, 512, 128], act=C.ELEM_FLOAT) == (C.MOE_OK, 0)
+    st, h = create(lib, "MoE", k=2, activation_type=2)
+    assert st == C.MOE_OK
+    try:
+        assert prepack_size(lib, h, 2, [8, 512, 256], et=C.ELEM_FLOAT16) == (C.MOE_OK, 0)
+    finally:
+        lib.moe_kernel_release(h)
+
+
+@pytest.mark.parametrize("idx,dims,et,act", [
+    (3, [8, 512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),   # a scale input
+    (0, [16, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16),
+    (2, [512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),      # not 3D
+    (2, [8, 512, 128], C.ELEM_FLOAT16, C.ELEM_FLOAT16),  # not uint8
+    (2, [8, 512, 128], C.ELEM_UINT8, C.ELEM_UINT8),      # act_type not a float type
+])
+def test_prepack_rejects_bad_arguments(lib, qkernel, idx, dims, et, act):
+    st, _ = prepack_size(lib, qkernel, idx, dims, act=act, et=et)
+    assert st == C.MOE_INVALID_ARGUMENT
+
+
+def test_prepack_not_packed_writes_nothing(lib, qkernel):
+    # an input the kernel keeps row-major: OK, *is_packed = 0, no device work
+    t = tensor([8, 520, 128], C.ELEM_UINT8)
+    flag = ctypes.c_int32(7)
+    st = lib.moe_kernel_prepack(qkernel, 2, ctypes.byref(t), C.ELEM_FLOAT16, None, 0, None, ctypes.byref(flag))
+    assert st == C.MOE_OK and flag.value == 0
+
+
+def test_prepack_rejects_small_buffer(lib, qkernel):
+    t = tensor([8, 512, 128], C.ELEM_UINT8)
+    flag = ctypes.c_int32(7)
+    st = lib.moe_kernel_prepack(qkernel, 2, ctypes.byref(t), C.ELEM_FLOAT16, ctypes.c_void_p(FAKE), 100, None,
+                                ctypes.byref(flag))
+    assert st == C.MOE_INVALID_ARGUMENT and flag.value == 0
+    assert b"too small" in lib.moe_last_error()

@@ -1,0 +1,139 @@
+"""Pre-packed (tile-major) QMoE expert weights on the GPU.
+
+The pack kernel's output is compared byte for byte with a numpy statement of
+the layout (onnxruntime-musa_amd/csrc/moe_prepack.hip).  The op reading
+pre-packed weights is compared with the same op reading the row-major
+weights: the kernels add the same products in the same order and only the
+load addresses differ, so the outputs must be bit-identical.  Full-size
+configurations are also checked against the oracle with pre-packed weights.
+"""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from moe_testutil import check_problem
+from onnxruntime_musa_amd import MoeError
+from onnxruntime_musa_amd.workloads import CONFIGS, make_problem, to_host
+
+pytestmark = pytest.mark.gpu
+
+C2, C3 = CONFIGS["c2_qmoe_int8_mixtral"], CONFIGS["c3_qmoe_int4_mixtral"]
+
+
+def pack_reference(w: np.ndarray, bits: int) -> np.ndarray:
+    """Tile-major layout: one block of 16 * cb bytes per (16-row tile, chunk
+    of 128 k), cb = 64 (int4) or 128 (int8) bytes of a row per chunk; the
+    16-byte piece q of row r of the tile sits at slot (q % kv) * 64 + (q //
+    kv) * 16 + r of the block, kv = cb / 64."""
+    E, N, rb = w.shape
+    cb = 64 if bits == 4 else 128
+    kv, cp, nch = cb // 64, cb // 16, rb // cb
+    pieces = w.reshape(E * N // 16, 16, nch, cp, 16)  # tile, row, chunk, piece, byte
+    out = np.empty((E * N // 16, nch, cb, 16), np.uint8)  # tile, chunk, slot, byte
+    for q in range(cp):
+        for r in range(16):
+            out[:, :, (q % kv) * 64 + (q // kv) * 16 + r, :] = pieces[:, r, :, q, :]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("cfg", [C2, C3], ids=["int8", "int4"])
+@pytest.mark.parametrize("idx", [2, 5, 8])
+def test_pack_layout(cuda, cfg, idx):
+    p = make_problem(cfg, 4, seed=11, device=cuda, gen="numpy", hidden=256, inter=384)
+    op = p.make_op()
+    w = p.schema_inputs()[idx]
+    packed = op.prepack(idx, w, torch.float16)
+    torch.cuda.synchronize()
+    assert packed is not None
+    np.testing.assert_array_equal(packed.cpu().numpy(), pack_reference(to_host(w), cfg.bits))
+
+
+VARIANTS = {
+    "int8-chan-fc3": (C2, dict(hidden=256, inter=512)),
+    "int4-b128-fc3": (C3, dict(hidden=256, inter=512)),
+    "int4-b64-f32-bf16": (C3, dict(hidden=384, inter=256, block_size=64, scale_dtype="f32", dtype="bf16")),
+    "int8-b32-bf16": (C2, dict(hidden=256, inter=384, block_size=32, scale_dtype="bf16", dtype="bf16")),
+    "int4-b16": (C3, dict(hidden=256, inter=256, block_size=16)),
+    "int4-chunked-bias": (C3, dict(hidden=256, inter=512, use_fc3=False, swiglu_fusion=2, bias=True)),
+    "int8-silu": (C2, dict(hidden=256, inter=384, use_fc3=False, activation="silu", bias=True)),
+    "int4-fc2-slices": (C3, dict(hidden=512, inter=8192, experts=4)),
+}
+
+
+def run_pair(p, path):
+    inputs = p.schema_inputs()
+    plain, packed = p.make_op(expert_path=path), p.make_op(expert_path=path)
+    done = packed.prepack_all(*inputs)
+    y0, y1 = plain(*inputs), packed(*inputs)
+    torch.cuda.synchronize()
+    return done, y0, y1
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+@pytest.mark.parametrize("path,T", [("decode", 1), ("decode", 16), ("decode", 40), ("decode", 64),
+                                    ("prefill", 17), ("prefill", 300), ("auto", 130)])
+def test_packed_equals_row_major(cuda, name, path, T):
+    cfg, over = VARIANTS[name]
+    p = make_problem(replace(cfg, **over), T, seed=T + 5, device=cuda, gen="numpy")
+    done, y0, y1 = run_pair(p, path)
+    assert done, "nothing was packed"
+    assert torch.equal(y0, y1), f"{name} T={T} {path}: max diff {(y0.float() - y1.float()).abs().max().item()}"
+
+
+def test_packed_inputs_may_be_absent(cuda):
+    p = make_problem(replace(C3, hidden=256, inter=512), 16, seed=3, device=cuda, gen="numpy")
+    inputs = p.schema_inputs()
+    op = p.make_op()
+    y0 = op(*inputs).clone()
+    assert op.prepack_all(*inputs) == [2, 5, 8]
+    y1 = op(*inputs).clone()
+    none = [None if i in (2, 5, 8) else t for i, t in enumerate(inputs)]
+    y2 = op(*none)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1) and torch.equal(y0, y2)
+
+
+def test_packed_rejects_other_shape(cuda):
+    p = make_problem(replace(C3, hidden=256, inter=512), 16, seed=3, device=cuda, gen="numpy")
+    inputs = p.schema_inputs()
+    op = p.make_op()
+    op.prepack_all(*inputs)
+    other = make_problem(replace(C3, hidden=256, inter=256), 16, seed=3, device=cuda, gen="numpy").schema_inputs()
+    with pytest.raises(MoeError) as ei:
+        op(*inputs[:5], other[5], *inputs[6:])
+    assert ei.value.code == 2
+
+
+def test_packed_needs_an_mfma_path(cuda):
+    p = make_problem(replace(C3, hidden=256, inter=512), 8, seed=3, device=cuda, gen="numpy")
+    inputs = p.schema_inputs()
+    op = p.make_op(expert_path="simt")
+    op.prepack_all(*inputs)
+    with pytest.raises(MoeError) as ei:
+        op(*inputs)
+    assert ei.value.code == 9
+
+
+def test_fc1_and_fc3_pack_together(cuda):
+    p = make_problem(replace(C3, hidden=256, inter=512), 8, seed=3, device=cuda, gen="numpy")
+    inputs = p.schema_inputs()
+    op = p.make_op()
+    assert op.prepack(2, inputs[2], torch.float16) is not None
+    with pytest.raises(MoeError) as ei:
+        op(*inputs)
+    assert ei.value.code == 9
+
+
+@pytest.mark.parametrize("name,T", [("c3_qmoe_int4_mixtral", 16), ("c3_qmoe_int4_mixtral", 1),
+                                    ("c2_qmoe_int8_mixtral", 16), ("c2_qmoe_int8_mixtral", 1)])
+def test_full_decode_prepacked(cuda, name, T):
+    p = make_problem(CONFIGS[name], T, seed=300 + T, device=cuda)
+    check_problem(p, threads=16, prepack=True)
+
+
+@pytest.mark.parametrize("name", ["c2_qmoe_int8_mixtral", "c3_qmoe_int4_mixtral"])
+def test_full_prefill_prepacked(cuda, name):
+    p = make_problem(CONFIGS[name], 4096, seed=4097, device=cuda)
+    check_problem(p, sample_tokens=48, threads=16, prepack=True)
