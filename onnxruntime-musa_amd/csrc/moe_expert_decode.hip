@@ -184,7 +184,12 @@ decode::Stage fc2_stage(const ExpertArgs& a) {
 
 }  // namespace
 
-hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
+bool decode_routes_in_fc1(const ExpertArgs& a) {
+  if (a.T * a.k > decode::kFusedRouteRows || a.E > decode::kFusedRouteExperts) return false;
+  return plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode).stream1;
+}
+
+hipError_t launch_fc1_decode(const ExpertArgs& a, const moe_route_params* route, hipStream_t stream) {
   const bool gated = a.gate_mode != kGateNone;
   decode::Stage st = fc1_stage(a);
   const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
@@ -195,8 +200,14 @@ hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream) {
     ss.nslices = 1;
     ss.E = static_cast<int32_t>(a.E);
     ss.ngroups = decode::stream_groups(a.T, a.E, a.k);
+    if (route) {
+      if (!decode_routes_in_fc1(a)) return hipErrorInvalidValue;
+      ss.route = *route;
+      ss.route_ints = static_cast<int32_t>(a.E + 1 + a.T * a.k);
+    }
     return decode::dispatch_stream(ss, a, true, gated, stream);
   }
+  if (route) return hipErrorInvalidValue;
   decode::pick_splits(st, a, gated, false);
   return decode::dispatch(st, a, true, gated, stream);
 }

@@ -126,10 +126,51 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
     for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
     return;
   }
+  const int64_t plane = a.T * a.k * a.H;
+  // Up to kFinLoads (slot, plane) values per thread: every load is issued
+  // before the first sum (a decode layer's y2 planes are in L2, so the
+  // time is load latency), then the sums run in the order of the loop below.
+  constexpr int kFinLoads = 16;
+  if ((a.H % 4) == 0 && a.k * a.y2_planes <= kFinLoads) {
+    const int np = a.y2_planes, nl = static_cast<int>(a.k) * np;
+    float4 v[kFinLoads];
+#pragma unroll
+    for (int i = 0; i < kFinLoads; ++i) {
+      if (i < nl) {
+        const int j = i / np, z = i - j * np;
+        v[i] = *reinterpret_cast<const float4*>(a.y2 + z * plane + static_cast<int64_t>(a.inv_perm[t * a.k + j]) * a.H + h0);
+      }
+    }
+    float4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kFinLoads; ++i) {
+      if (i < nl) {
+        const int j = i / np, z = i - j * np;
+        if (z == 0) {
+          s = v[i];
+        } else {
+          s.x += v[i].x;
+          s.y += v[i].y;
+          s.z += v[i].z;
+          s.w += v[i].w;
+        }
+        if (z == np - 1) {
+          const float w = a.topk_w[t * a.k + j];
+          acc[0] += w * s.x;
+          acc[1] += w * s.y;
+          acc[2] += w * s.z;
+          acc[3] += w * s.w;
+        }
+      }
+    }
+    typename OT::storage* out = static_cast<typename OT::storage*>(a.out);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
+    return;
+  }
   for (int64_t j = 0; j < a.k; ++j) {
     const int64_t f = t * a.k + j;
     const float w = a.topk_w[f];
-    const int64_t plane = a.T * a.k * a.H;
     const float* y = a.y2 + static_cast<int64_t>(a.inv_perm[f]) * a.H;
     if (h0 + 4 <= a.H && (a.H % 4) == 0) {
       float4 v = *reinterpret_cast<const float4*>(y + h0);

@@ -49,6 +49,7 @@
 #include <type_traits>
 
 #include "moe_expert_decode.h"
+#include "moe_route_device.h"
 
 namespace moe {
 namespace decode {
@@ -71,7 +72,18 @@ struct StreamStage {
   int32_t nslices;  // K slices (fc2 partial planes)
   int32_t E;        // experts
   int32_t ngroups;  // bound on the row groups of all experts: E + T*k/16
+  // fc1 only: with route.logits set, every workgroup routes and dispatches
+  // the batch itself in its prologue (into LDS: E + 1 offsets and T k rows,
+  // route_ints in all) and workgroup 0 publishes the results to route's
+  // outputs; otherwise offsets and perm come from the router kernels.
+  moe_route_params route;
+  int32_t route_ints;
 };
+
+// Largest T * k and expert count for which the decode fc1 kernel routes in
+// its prologue.
+constexpr int kFusedRouteRows = 1024;
+constexpr int kFusedRouteExperts = 64;
 
 template <int WF, bool GATED>
 struct SGeo {
@@ -156,9 +168,11 @@ inline int32_t stream_groups(int64_t T, int64_t E, int64_t k) {
   return static_cast<int32_t>(std::min(E, rows) + (rows + kStreamRows - 1) / kStreamRows);
 }
 
-// Bytes of dynamic LDS of the stream kernel (ngroups: row-group list entries).
-inline size_t stream_lds_bytes(int ksc, int ngroups, int nw) {
-  const size_t ex = (static_cast<size_t>(ngroups) * 4 + 15) / 16 * 16;
+// Bytes of dynamic LDS of the stream kernel (ngroups: row-group list
+// entries; route_ints: routing results kept in LDS, 0 when the router
+// kernels route).  The routing scratch of the prologue overlays the slice.
+inline size_t stream_lds_bytes(int ksc, int ngroups, int nw, int route_ints) {
+  const size_t ex = (static_cast<size_t>(ngroups) * 4 + 15) / 16 * 16 + (static_cast<size_t>(route_ints) * 4 + 15) / 16 * 16;
   const size_t act = static_cast<size_t>(kStreamRows) * (static_cast<size_t>(ksc) * 256 + 16) +
                      static_cast<size_t>(ksc) * kStreamRows * 4;
   const size_t slots = static_cast<size_t>(nw) * 2 * 64 * 16;
@@ -201,10 +215,25 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   const int ksc = ss.ksc, nsl = ss.nslices, E = ss.E;
   const int pitch = ksc * 256 + 16;
   int* exl = reinterpret_cast<int*>(smem);  // row groups: expert | (group << 16), ascending
-  uint8_t* region = smem + (ss.ngroups * 4 + 15) / 16 * 16;
+  int* lroute = reinterpret_cast<int*>(smem + (ss.ngroups * 4 + 15) / 16 * 16);  // [E + 1] offsets, [T k] perm
+  uint8_t* region = smem + (ss.ngroups * 4 + 15) / 16 * 16 + (ss.route_ints * 4 + 15) / 16 * 16;
   uint8_t* xs = region;                                         // [16][pitch] activation slice
   float* corr = reinterpret_cast<float*>(region + 16 * pitch);  // [ksc][16] bias sums per chunk and row
   float* slots = reinterpret_cast<float*>(region);              // [NW][WT][64] float4, after the compute
+
+  // ---- routing (fc1 of a small batch): every workgroup computes the same
+  // top-k, counts, offsets and stable permutation into LDS (the scratch
+  // overlays the activation slice, not yet in use); workgroup 0 also writes
+  // them out for fc2 and finalize ----
+  const int32_t* offs = p.offsets;
+  const int32_t* perm = p.perm;
+  if constexpr (FC1) {
+    if (ss.route.logits) {
+      route_dispatch_block<AT>(ss.route, lroute, lroute + E + 1, reinterpret_cast<int*>(region), blockIdx.x == 0);
+      offs = lroute;
+      perm = lroute + E + 1;
+    }
+  }
 
   // ---- row groups: each routed expert's rows in groups of 16 (the MFMA M);
   // an expert with more rows streams its weights once per group.
@@ -212,7 +241,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   int e_act = 0;
   for (int base = 0; base < E; base += NT) {
     const int e = base + tid;
-    const int cnt = e < E ? p.offsets[e + 1] - p.offsets[e] : 0;
+    const int cnt = e < E ? offs[e + 1] - offs[e] : 0;
     const int nv = (cnt + kStreamRows - 1) / kStreamRows;
     int inc = nv;  // inclusive scan over the wave
 #pragma unroll
@@ -321,8 +350,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int b0 = nb * wave / NW, b1 = nb * (wave + 1) / NW;
     const int ent = __builtin_amdgcn_readfirstlane(exl[a]);
     const int e = ent & 0xFFFF;
-    const int row0 = __builtin_amdgcn_readfirstlane(p.offsets[e]) + (ent >> 16) * kStreamRows;
-    const int cnt = __builtin_amdgcn_readfirstlane(p.offsets[e + 1]) - row0;
+    const int row0 = __builtin_amdgcn_readfirstlane(offs[e]) + (ent >> 16) * kStreamRows;
+    const int cnt = __builtin_amdgcn_readfirstlane(offs[e + 1]) - row0;
     const int nrows = cnt < kStreamRows ? cnt : kStreamRows;
     const int cs0 = s * ksc;  // first chunk of the slice
 
@@ -400,7 +429,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int gpr = ksc / 4;        // 1 KB groups per row
     const int ngr = nrows * gpr;    // groups of the slice
     // source row of row m (fc1: the token of dispatched row row0 + m), lane m
-    const int srcl = FC1 ? (lane < nrows ? p.perm[row0 + lane] / static_cast<int>(p.topk) : 0) : row0 + lane;
+    const int srcl = FC1 ? (lane < nrows ? perm[row0 + lane] / static_cast<int>(p.topk) : 0) : row0 + lane;
     for (int q = wave; q < ngr; q += NW) {
       const int m = q / gpr, r = (q - m * gpr) * 64 + lane;  // row, piece in the row
       const int64_t k = static_cast<int64_t>(cs0 + (r >> 4)) * kChunk + (r & 15) * 8;
@@ -733,7 +762,7 @@ template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATE
 hipError_t launch_stream(const StreamStage& ss, hipStream_t stream) {
   using G = SGeo<WF, GATED>;
   auto kern = gemv_stream_kernel<AT, WF, SM, ST, NSC, FC1, GATED>;
-  const size_t lds = stream_lds_bytes(ss.ksc, ss.ngroups, G::NW);  // <= 152 KB + the group list
+  const size_t lds = stream_lds_bytes(ss.ksc, ss.ngroups, G::NW, ss.route_ints);  // <= 157 KB
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(stream_grid(G::NW))), dim3(G::NW * 64), lds, stream, ss);
   return hipGetLastError();
 }

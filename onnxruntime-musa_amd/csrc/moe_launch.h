@@ -74,7 +74,10 @@ struct ExpertArgs {
 
 hipError_t launch_fc1_simt(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream);
-hipError_t launch_fc1_decode(const ExpertArgs& a, hipStream_t stream);
+// route: when non-null, the fc1 kernel routes and dispatches the batch in its
+// prologue and writes route's outputs (decode_routes_in_fc1 says when it can).
+hipError_t launch_fc1_decode(const ExpertArgs& a, const moe_route_params* route, hipStream_t stream);
+bool decode_routes_in_fc1(const ExpertArgs& a);
 hipError_t launch_fc2_decode(const ExpertArgs& a, int* y2_planes, hipStream_t stream);
 hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half, hipStream_t stream);

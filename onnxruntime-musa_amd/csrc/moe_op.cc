@@ -617,13 +617,17 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     auto mark = [&](int i) {
       if (prof && e == hipSuccess) e = hipEventRecord(mk->ev[i], stream);
     };
+    // small decode batches are routed inside the fc1 kernel (one launch less)
+    const bool route_in_fc1 = path == moe::kPathDecode && moe::decode_routes_in_fc1(a);
     mark(0);
-    e = e == hipSuccess ? moe::launch_route_dispatch(ra, stream) : e;
-    if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+    if (!route_in_fc1) {
+      e = e == hipSuccess ? moe::launch_route_dispatch(ra, stream) : e;
+      if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+    }
     mark(1);
     switch (path) {
       case moe::kPathDecode:
-        e = moe::launch_fc1_decode(a, stream);
+        e = moe::launch_fc1_decode(a, route_in_fc1 ? &ra.p : nullptr, stream);
         mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_decode(a, &a.y2_planes, stream);
         break;

@@ -1,0 +1,200 @@
+// moe_route_device.h -- per-token routing and stable-rank helpers shared by
+// the router/dispatch kernels and the decode kernel that routes in its
+// prologue.
+//
+// Routing: one 64-lane wavefront per token; each lane holds up to 8 logits
+// (expert e = lane + 64 i); the k experts are chosen by k rounds of a wave
+// arg-max under the order (logit desc, expert id asc) -- the reference's
+// TopK tie rule (musa/ep/src/kernels/math/topk_impl.mu:46-65: equal values
+// -> lower index).
+#pragma once
+
+#include <limits.h>
+
+#include "moe_device.h"
+#include "moe_mi355x.h"
+
+namespace moe {
+
+__device__ __forceinline__ bool cand_before(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// NaN logits rank below every number (as -inf), so every arg-max round finds
+// a valid expert.
+template <typename LT>
+__device__ __forceinline__ float load_logit(const void* p, int64_t i) {
+  const float v = to_f32<LT>(static_cast<const typename LT::storage*>(p)[i]);
+  return v != v ? -INFINITY : v;
+}
+
+// Routes one token with the calling wavefront.  Returns, in lanes j < k, the
+// j-th chosen expert id and its weight.
+template <typename LT, int VPL>
+__device__ __forceinline__ void route_token(const void* logits, int64_t t, int E, int k,
+                                            bool normalize, bool sigm, int lane,
+                                            int* out_id, float* out_w) {
+  float v[VPL];
+  bool taken[VPL];
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int e = lane + kWave * i;
+    v[i] = e < E ? load_logit<LT>(logits, t * E + e) : -INFINITY;
+    taken[i] = e >= E;
+    if (e < E) m = fmaxf(m, v[i]);
+  }
+  float s = 0.0f;
+  if (!sigm) {
+    m = wave_max(m);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (!taken[i]) s += expf(v[i] - m);
+    s = wave_sum(s);
+  }
+  int my_id = 0;
+  float my_p = 0.0f, wsum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int bid = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = lane + kWave * i;
+      if (!taken[i] && cand_before(v[i], e, bv, bid)) {
+        bv = v[i];
+        bid = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, kWave);
+      const int oid = __shfl_xor(bid, o, kWave);
+      if (cand_before(ov, oid, bv, bid)) {
+        bv = ov;
+        bid = oid;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+      if (lane + kWave * i == bid) taken[i] = true;
+    const float p = sigm ? 1.0f / (1.0f + expf(-bv)) : expf(bv - m) / s;
+    wsum += p;
+    if (lane == j) {
+      my_id = bid;
+      my_p = p;
+    }
+  }
+  *out_id = my_id;
+  *out_w = normalize ? my_p / wsum : my_p;
+}
+
+// Ballot-built mask of the lanes (among `active`) holding the same expert id.
+__device__ __forceinline__ uint64_t match_mask(int e, bool active, int nbits) {
+  uint64_t mask = __ballot(active);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t bal = __ballot(active && bit);
+    mask &= bit ? bal : ~bal;
+  }
+  return mask;
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t mask, int lane) {
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  return __popcll(mask & below);
+}
+
+__device__ __forceinline__ int id_bits(int E) {
+  int b = 0;
+  while ((1 << b) < E) ++b;
+  return b;
+}
+
+// Routing and dispatch of a small batch by one workgroup, results in LDS:
+// offs[0..E] (exclusive scan of the per-expert counts) and perm[0..T k)
+// (row -> flat index t k + j, expert-major, ascending flat index within an
+// expert): the values the router/dispatch kernels produce.  With publish,
+// the workgroup also writes topk_ids, topk_w, offsets, perm and inv_perm of
+// p to global memory.  scratch: LDS of (2 E + nwaves E + T k) ints.  Needs
+// E <= 64 (one expert per lane in the scan); every thread of the workgroup
+// calls it.
+template <typename LT>
+__device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* perm, int* scratch,
+                                     bool publish) {
+  const int E = static_cast<int>(p.num_experts), k = static_cast<int>(p.k);
+  const int T = static_cast<int>(p.num_tokens), n = T * k;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int nwaves = blockDim.x / kWave;
+  int* cnt = scratch;
+  int* base = cnt + E;
+  int* wcnt = base + E;
+  int* ids = wcnt + nwaves * E;
+  for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  for (int t = wave; t < T; t += nwaves) {
+    int id;
+    float w;
+    route_token<LT, 1>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
+    if (lane < k) {
+      ids[t * k + lane] = id;
+      atomicAdd(&cnt[id], 1);  // counts only; order-independent
+      if (publish) {
+        p.topk_ids[t * k + lane] = id;
+        p.topk_w[t * k + lane] = w;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int c = lane < E ? cnt[lane] : 0;
+    int inc = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += v;
+    }
+    if (lane < E) {
+      offs[lane] = inc - c;
+      base[lane] = inc - c;
+      if (publish) p.offsets[lane] = inc - c;
+    }
+    if (lane == kWave - 1) {
+      offs[E] = inc;
+      if (publish) p.offsets[E] = inc;
+    }
+  }
+  __syncthreads();
+  // stable ranks: within a wave from a ballot-built match mask, across waves
+  // from per-wave counts; no unordered atomic decides a position
+  const int nbits = id_bits(E);
+  for (int s0 = 0; s0 < n; s0 += blockDim.x) {
+    for (int i = tid; i < nwaves * E; i += blockDim.x) wcnt[i] = 0;
+    __syncthreads();
+    const int f = s0 + tid;
+    const bool active = f < n;
+    const int e = active ? ids[f] : 0;
+    const uint64_t mm = match_mask(e, active, nbits);
+    const int r = lanes_below(mm, lane);
+    if (active && r == 0) wcnt[wave * E + e] = __popcll(mm);
+    __syncthreads();
+    if (active) {
+      int before = 0;
+      for (int w = 0; w < wave; ++w) before += wcnt[w * E + e];
+      const int row = base[e] + before + r;
+      perm[row] = f;
+      if (publish) {
+        p.perm[row] = f;
+        p.inv_perm[f] = row;
+      }
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += blockDim.x) {
+      int add = 0;
+      for (int w = 0; w < nwaves; ++w) add += wcnt[w * E + x];
+      base[x] += add;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace moe

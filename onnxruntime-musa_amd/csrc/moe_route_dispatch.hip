@@ -22,97 +22,10 @@
 
 #include "moe_device.h"
 #include "moe_launch.h"
+#include "moe_route_device.h"
 
 namespace moe {
 namespace {
-
-__device__ __forceinline__ bool cand_before(float va, int ia, float vb, int ib) {
-  return va > vb || (va == vb && ia < ib);
-}
-
-// NaN logits rank below every number (as -inf), so every arg-max round finds
-// a valid expert.
-template <typename LT>
-__device__ __forceinline__ float load_logit(const void* p, int64_t i) {
-  const float v = to_f32<LT>(static_cast<const typename LT::storage*>(p)[i]);
-  return v != v ? -INFINITY : v;
-}
-
-// Routes one token with the calling wavefront.  Returns, in lanes j < k, the
-// j-th chosen expert id and its weight.
-template <typename LT, int VPL>
-__device__ __forceinline__ void route_token(const void* logits, int64_t t, int E, int k,
-                                            bool normalize, bool sigm, int lane,
-                                            int* out_id, float* out_w) {
-  float v[VPL];
-  bool taken[VPL];
-  float m = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int e = lane + kWave * i;
-    v[i] = e < E ? load_logit<LT>(logits, t * E + e) : -INFINITY;
-    taken[i] = e >= E;
-    if (e < E) m = fmaxf(m, v[i]);
-  }
-  float s = 0.0f;
-  if (!sigm) {
-    m = wave_max(m);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i)
-      if (!taken[i]) s += expf(v[i] - m);
-    s = wave_sum(s);
-  }
-  int my_id = 0;
-  float my_p = 0.0f, wsum = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int bid = INT_MAX;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int e = lane + kWave * i;
-      if (!taken[i] && cand_before(v[i], e, bv, bid)) {
-        bv = v[i];
-        bid = e;
-      }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oid = __shfl_xor(bid, o, kWave);
-      if (cand_before(ov, oid, bv, bid)) {
-        bv = ov;
-        bid = oid;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i)
-      if (lane + kWave * i == bid) taken[i] = true;
-    const float p = sigm ? 1.0f / (1.0f + expf(-bv)) : expf(bv - m) / s;
-    wsum += p;
-    if (lane == j) {
-      my_id = bid;
-      my_p = p;
-    }
-  }
-  *out_id = my_id;
-  *out_w = normalize ? my_p / wsum : my_p;
-}
-
-// Ballot-built mask of the lanes (among `active`) holding the same expert id.
-__device__ __forceinline__ uint64_t match_mask(int e, bool active, int nbits) {
-  uint64_t mask = __ballot(active);
-  for (int b = 0; b < nbits; ++b) {
-    const bool bit = (e >> b) & 1;
-    const uint64_t bal = __ballot(active && bit);
-    mask &= bit ? bal : ~bal;
-  }
-  return mask;
-}
-
-__device__ __forceinline__ int lanes_below(uint64_t mask, int lane) {
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-  return __popcll(mask & below);
-}
 
 // Stable scatter of flat entries [f0, f1) by the whole workgroup.  base[e]
 // (LDS) holds the next free row of expert e and is advanced here.  wcnt is an
@@ -193,12 +106,6 @@ __device__ void scan_experts(const int* cnt, int E, int* base, int32_t* offsets,
     offsets[E] = inc;
     if (tile_offsets) tile_offsets[E] = tinc;
   }
-}
-
-__device__ __forceinline__ int id_bits(int E) {
-  int b = 0;
-  while ((1 << b) < E) ++b;
-  return b;
 }
 
 // ---- small T: everything in one workgroup (1024 threads) ----
