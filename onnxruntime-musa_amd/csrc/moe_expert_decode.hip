@@ -186,7 +186,10 @@ decode::Stage fc2_stage(const ExpertArgs& a) {
 
 bool decode_routes_in_fc1(const ExpertArgs& a) {
   if (a.T * a.k > decode::kFusedRouteRows || a.E > decode::kFusedRouteExperts) return false;
-  return plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode).stream1;
+  const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
+  // the routing scratch overlays the activation-slice region (bounds over
+  // both wave counts of the stream kernel: 8 and 12 waves)
+  return pl.stream1 && route_block_scratch_bytes(a.T, a.E, a.k, 12, 2) <= decode::stream_region_bytes(pl.ksc1, 8);
 }
 
 hipError_t launch_fc1_decode(const ExpertArgs& a, const moe_route_params* route, hipStream_t stream) {

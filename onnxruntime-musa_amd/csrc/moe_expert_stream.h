@@ -171,12 +171,15 @@ inline int32_t stream_groups(int64_t T, int64_t E, int64_t k) {
 // Bytes of dynamic LDS of the stream kernel (ngroups: row-group list
 // entries; route_ints: routing results kept in LDS, 0 when the router
 // kernels route).  The routing scratch of the prologue overlays the slice.
-inline size_t stream_lds_bytes(int ksc, int ngroups, int nw, int route_ints) {
-  const size_t ex = (static_cast<size_t>(ngroups) * 4 + 15) / 16 * 16 + (static_cast<size_t>(route_ints) * 4 + 15) / 16 * 16;
+inline size_t stream_region_bytes(int ksc, int nw) {
   const size_t act = static_cast<size_t>(kStreamRows) * (static_cast<size_t>(ksc) * 256 + 16) +
                      static_cast<size_t>(ksc) * kStreamRows * 4;
   const size_t slots = static_cast<size_t>(nw) * 2 * 64 * 16;
-  return ex + std::max(act, slots);
+  return std::max(act, slots);
+}
+inline size_t stream_lds_bytes(int ksc, int ngroups, int nw, int route_ints) {
+  const size_t ex = (static_cast<size_t>(ngroups) * 4 + 15) / 16 * 16 + (static_cast<size_t>(route_ints) * 4 + 15) / 16 * 16;
+  return ex + stream_region_bytes(ksc, nw);
 }
 
 // NSC: folded scales (block 16/32/64): elements per lane and chunk (2 for

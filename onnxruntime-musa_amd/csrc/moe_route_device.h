@@ -115,9 +115,18 @@ __device__ __forceinline__ int id_bits(int E) {
 // (row -> flat index t k + j, expert-major, ascending flat index within an
 // expert): the values the router/dispatch kernels produce.  With publish,
 // the workgroup also writes topk_ids, topk_w, offsets, perm and inv_perm of
-// p to global memory.  scratch: LDS of (2 E + nwaves E + T k) ints.  Needs
+// p to global memory.  scratch: route_block_scratch_bytes() of LDS.  Needs
 // E <= 64 (one expert per lane in the scan); every thread of the workgroup
 // calls it.
+//
+// The logits are first copied to LDS with one load per element: when every
+// workgroup of a grid routes the same batch, a load per token and wave would
+// send thousands of requests for the same few cache lines to one L2 channel.
+// LDS bytes route_dispatch_block needs as scratch.
+inline size_t route_block_scratch_bytes(int64_t T, int64_t E, int64_t k, int nwaves, int logit_bytes) {
+  return static_cast<size_t>((2 * E + nwaves * E + T * k) * 4 + T * E * logit_bytes);
+}
+
 template <typename LT>
 __device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* perm, int* scratch,
                                      bool publish) {
@@ -129,18 +138,60 @@ __device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* 
   int* base = cnt + E;
   int* wcnt = base + E;
   int* ids = wcnt + nwaves * E;
+  using LS = typename LT::storage;
+  LS* xl = reinterpret_cast<LS*>(ids + n);  // [T][E] logits
+  const LS* xg = static_cast<const LS*>(p.logits);
+  for (int i = tid; i < T * E; i += blockDim.x) xl[i] = xg[i];
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  for (int t = wave; t < T; t += nwaves) {
-    int id;
-    float w;
-    route_token<LT, 1>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
-    if (lane < k) {
-      ids[t * k + lane] = id;
-      atomicAdd(&cnt[id], 1);  // counts only; order-independent
+  // Tokens in lane groups of G = the power of two >= E (64 / G tokens per
+  // wave): the same steps as route_token with log2(G) butterfly steps instead
+  // of 6.  Lanes past E hold -inf / 0, which the omitted steps of a full-wave
+  // butterfly would only have added or compared, so the sums and the chosen
+  // experts are bit-identical to route_token's.
+  const int G = E <= 8 ? 8 : (E <= 16 ? 16 : (E <= 32 ? 32 : 64));
+  const int tpw = kWave / G, e = lane % G;
+  const bool sigm = p.sigmoid != 0;
+  for (int t0 = wave * tpw; t0 < T; t0 += nwaves * tpw) {
+    const int t = t0 + lane / G;
+    const bool valid = t < T && e < E;
+    const float v = valid ? load_logit<LT>(xl, static_cast<int64_t>(t) * E + e) : -INFINITY;
+    bool taken = !valid;
+    float m = v;
+    for (int o = G / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, G));
+    float sum = 0.0f;
+    if (!sigm) {
+      sum = valid ? expf(v - m) : 0.0f;
+      for (int o = G / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, G);
+    }
+    int my_id = 0;
+    float my_p = 0.0f, wsum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      float bv = taken ? -INFINITY : v;
+      int bid = taken ? INT_MAX : e;
+      for (int o = G / 2; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, G);
+        const int oid = __shfl_xor(bid, o, G);
+        if (cand_before(ov, oid, bv, bid)) {
+          bv = ov;
+          bid = oid;
+        }
+      }
+      if (e == bid) taken = true;
+      const float pj = sigm ? 1.0f / (1.0f + expf(-bv)) : expf(bv - m) / sum;
+      wsum += pj;
+      if (e == j) {
+        my_id = bid;
+        my_p = pj;
+      }
+    }
+    if (t < T && e < k) {
+      const float w = p.normalize != 0 ? my_p / wsum : my_p;
+      ids[t * k + e] = my_id;
+      atomicAdd(&cnt[my_id], 1);  // counts only; order-independent
       if (publish) {
-        p.topk_ids[t * k + lane] = id;
-        p.topk_w[t * k + lane] = w;
+        p.topk_ids[t * k + e] = my_id;
+        p.topk_w[t * k + e] = w;
       }
     }
   }
