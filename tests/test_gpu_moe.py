@@ -51,6 +51,10 @@ QUANT_VARIANTS = [
     dict(bits=8, block_size=32, scale_dtype="bf16"),
     dict(bits=4, block_size=0, scale_dtype="f16"),
     dict(bits=4, block_size=16, scale_dtype="f16"),
+    dict(bits=4, block_size=32, scale_dtype="f16"),
+    dict(bits=4, block_size=32, scale_dtype="bf16"),
+    dict(bits=4, block_size=32, scale_dtype="f32"),
+    dict(bits=8, block_size=32, scale_dtype="f16"),
     dict(bits=4, block_size=64, scale_dtype="f32"),
     dict(bits=4, block_size=256, scale_dtype="f16"),
 ]
@@ -58,7 +62,7 @@ QUANT_VARIANTS = [
 
 @pytest.mark.parametrize("q", QUANT_VARIANTS, ids=lambda q: f"int{q['bits']}-bs{q['block_size']}-{q['scale_dtype']}")
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("path,T", [("decode", 9), ("prefill", 200)])
+@pytest.mark.parametrize("path,T", [("decode", 9), ("decode", 48), ("prefill", 200)])
 def test_quant_formats(cuda, q, dtype, path, T):
     p = make_problem(C3, T, seed=2, device=cuda, gen="numpy", hidden=256, inter=512, dtype=dtype, **q)
     check_problem(p, path)
@@ -69,7 +73,8 @@ def test_quant_formats(cuda, q, dtype, path, T):
     (C3, dict(hidden=256, inter=4096)),
     (C2, dict(hidden=256, inter=4096)),
     (C4, dict(hidden=256, inter=2880, experts=8)),
-], ids=["dense", "int4", "int8", "int4-bs32-bf16"])
+    (C4, dict(hidden=2880, inter=256, experts=8)),
+], ids=["dense", "int4", "int8", "int4-bs32-bf16", "int4-bs32-bf16-k2880-fc1"])
 @pytest.mark.parametrize("T", [1, 4, 16])
 def test_decode_long_k_groups(cuda, base, over, T):
     """Few experts and a long fc2 K: the decode path splits K across
