@@ -68,7 +68,10 @@ typedef enum moe_status {
 typedef enum moe_elem_type {
   MOE_ELEM_FLOAT = 1,
   MOE_ELEM_UINT8 = 2,
+  MOE_ELEM_INT32 = 6,   /* TopK only */
+  MOE_ELEM_INT64 = 7,   /* TopK only */
   MOE_ELEM_FLOAT16 = 10,
+  MOE_ELEM_DOUBLE = 11, /* TopK only */
   MOE_ELEM_BFLOAT16 = 16
 } moe_elem_type;
 
@@ -227,6 +230,33 @@ typedef struct moe_route_params {
 
 MOE_API size_t moe_route_dispatch_scratch_size(int64_t num_tokens, int64_t num_experts, int64_t k);
 MOE_API moe_status moe_route_dispatch_launch(const moe_route_params *params, void *stream);
+
+/* ------------------------------------------------------------------ */
+/* ONNX TopK (opsets 10-19) on the router's ordering rule: the k largest
+ * (largest = 1) or smallest (largest = 0) elements along one axis, ties
+ * toward the lower index, always in sorted order (sorted = 0 admits any
+ * order).  The input is viewed as [rows, dim, inner] with the axis in the
+ * middle; values [rows, k, inner] keep the input's type, indices are int64.
+ * Types: float, float16, bfloat16, double, int32, int64.  -0.0 ties with
+ * +0.0; NaN sorts above +inf.  Replaces the reference's TopK kernel launchers
+ * LaunchMusaTopK{PairReduce,BlockSort,...}Kernel(input, values, indices,
+ * MusaTopKParams{rows, dim, inner, k, largest, sorted}, elem_type, stream)
+ * (musa/ep/src/kernels/math/topk_impl.h:10-33,
+ * shared_inc/device_kernel_types.h:258-266) and their validation
+ * (musa/ep/src/kernels/math/topk.cc:133-200): k outside [0, dim] ->
+ * MOE_INVALID_ARGUMENT, an unsupported type or dim > 8192 ->
+ * MOE_NOT_IMPLEMENTED. */
+typedef struct moe_topk_params {
+  const void *input;
+  int32_t elem_type; /* moe_elem_type */
+  int32_t largest;
+  int32_t sorted;
+  int32_t pad_;
+  int64_t rows, dim, inner, k;
+  void *values;
+  int64_t *indices;
+} moe_topk_params;
+MOE_API moe_status moe_topk_launch(const moe_topk_params *params, void *stream);
 
 /* Library version string. */
 MOE_API const char *moe_version(void);

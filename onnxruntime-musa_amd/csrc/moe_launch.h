@@ -86,6 +86,15 @@ hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
 // Reorders row-major quantized weights [rows, row_bytes] (rows a multiple of
 // 16, row_bytes a multiple of the chunk row bytes cbytes = 64 for int4, 128
 // for int8) into the tile-major layout read by the decode and prefill kernels.
+// ONNX TopK over the middle axis of [rows, dim, inner] (moe_topk.hip).
+struct TopKArgs {
+  int64_t rows, dim, inner, k;
+  int32_t largest, sorted;
+};
+constexpr int64_t kTopKMaxDim = 8192;  // one workgroup sorts a slice in LDS
+hipError_t launch_topk(const void* in, int32_t elem_type, void* values, int64_t* indices, const TopKArgs& p,
+                       hipStream_t stream);
+
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
                           hipStream_t stream);
 

@@ -692,6 +692,32 @@ size_t moe_route_dispatch_scratch_size(int64_t num_tokens, int64_t num_experts, 
   return moe::route_scratch_bytes(num_tokens, num_experts, k);
 }
 
+moe_status moe_topk_launch(const moe_topk_params* p, void* stream) {
+  try {
+    if (!p) return fail(MOE_INVALID_ARGUMENT, "null params");
+    if (p->rows < 0 || p->dim < 0 || p->inner < 0) return fail(MOE_INVALID_ARGUMENT, "negative shape");
+    if (p->largest != 0 && p->largest != 1) return fail(MOE_INVALID_ARGUMENT, "TopK largest must be 0 or 1");
+    if (p->sorted != 0 && p->sorted != 1) return fail(MOE_INVALID_ARGUMENT, "TopK sorted must be 0 or 1");
+    if (p->k < 0 || p->k > p->dim) return fail(MOE_INVALID_ARGUMENT, "TopK K value is outside axis range");
+    switch (p->elem_type) {
+      case MOE_ELEM_FLOAT: case MOE_ELEM_FLOAT16: case MOE_ELEM_BFLOAT16:
+      case MOE_ELEM_DOUBLE: case MOE_ELEM_INT32: case MOE_ELEM_INT64: break;
+      default: return fail(MOE_NOT_IMPLEMENTED, "TopK unsupported dtype");
+    }
+    if (p->rows * p->inner == 0 || p->k == 0) return MOE_OK;
+    if (p->dim > moe::kTopKMaxDim)
+      return fail(MOE_NOT_IMPLEMENTED, "TopK axis longer than " + std::to_string(moe::kTopKMaxDim));
+    if (!p->input || !p->values || !p->indices) return fail(MOE_INVALID_ARGUMENT, "null tensor");
+    const moe::TopKArgs a{p->rows, p->dim, p->inner, p->k, p->largest, p->sorted};
+    const hipError_t e = moe::launch_topk(p->input, p->elem_type, p->values, p->indices, a,
+                                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "TopK launch");
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
 moe_status moe_route_dispatch_launch(const moe_route_params* params, void* stream) {
   if (!params) return fail(MOE_INVALID_ARGUMENT, "null params");
   const moe_route_params& p = *params;

@@ -1,0 +1,136 @@
+// moe_topk.hip -- the ONNX TopK op (opsets 10-19) for gfx950, built from the
+// router's ordering rule: values by key, ties toward the lower index
+// (musa/ep/src/kernels/math/topk_impl.mu:46-65).
+//
+// One workgroup per (row, inner) slice of the input viewed as [rows, dim,
+// inner].  The slice's dim elements become order-preserving integer keys in
+// LDS (floats: sign-magnitude bits flipped to two's-complement order, -0.0
+// folded onto +0.0 so that it ties with +0.0 as a value comparison does;
+// integers: sign bit flipped; smallest-first negates the key), padded to a
+// power of two with keys that sort last, and a bitonic network sorts (key
+// desc, index asc).  The first k entries are written out; values are read
+// back from the input at their index, so they keep their exact bits.
+//
+// NaN keys sort as the largest values (above +inf) for largest = 1 and the
+// smallest for largest = 0.
+#include <stdint.h>
+
+#include "moe_device.h"
+#include "moe_launch.h"
+
+namespace moe {
+namespace {
+
+template <typename T>
+__device__ __forceinline__ uint64_t topk_key(T v);
+// floats: flip all bits of negatives, set the sign bit of positives
+__device__ __forceinline__ uint64_t key_f64(double d) {
+  if (d == 0.0) d = 0.0;  // -0.0 ties with +0.0
+  const uint64_t b = __builtin_bit_cast(uint64_t, d);
+  return (b >> 63) ? ~b : (b | (uint64_t{1} << 63));
+}
+template <>
+__device__ __forceinline__ uint64_t topk_key<double>(double v) { return key_f64(v); }
+template <>
+__device__ __forceinline__ uint64_t topk_key<float>(float v) { return key_f64(static_cast<double>(v)); }
+template <>
+__device__ __forceinline__ uint64_t topk_key<_Float16>(_Float16 v) { return key_f64(static_cast<double>(static_cast<float>(v))); }
+template <>
+__device__ __forceinline__ uint64_t topk_key<uint16_t>(uint16_t v) {  // bf16 bits
+  return key_f64(static_cast<double>(bf16_to_f32(v)));
+}
+template <>
+__device__ __forceinline__ uint64_t topk_key<int32_t>(int32_t v) {
+  return static_cast<uint64_t>(static_cast<int64_t>(v)) ^ (uint64_t{1} << 63);
+}
+template <>
+__device__ __forceinline__ uint64_t topk_key<int64_t>(int64_t v) {
+  return static_cast<uint64_t>(v) ^ (uint64_t{1} << 63);
+}
+
+__device__ __forceinline__ bool entry_before(uint64_t ka, uint32_t ia, uint64_t kb, uint32_t ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T* __restrict__ values,
+                                                    int64_t* __restrict__ indices, TopKArgs p, int n) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint64_t* key = reinterpret_cast<uint64_t*>(smem);
+  uint32_t* idx = reinterpret_cast<uint32_t*>(smem + static_cast<size_t>(n) * 8);
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t slices = p.rows * p.inner;
+  for (int64_t sl = blockIdx.x; sl < slices; sl += gridDim.x) {
+    const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
+    const T* src = in + row * p.dim * p.inner + in0;
+    for (int i = tid; i < n; i += nt) {
+      if (i < p.dim) {
+        const uint64_t kv = topk_key<T>(src[static_cast<int64_t>(i) * p.inner]);
+        key[i] = p.largest ? kv : ~kv;
+        idx[i] = static_cast<uint32_t>(i);
+      } else {
+        key[i] = 0;            // after every element, ties broken by index
+        idx[i] = 0xFFFFFFFFu;
+      }
+    }
+    __syncthreads();
+    // bitonic network: segments of `size` alternate direction until the
+    // last merge, which leaves (key desc, index asc)
+    for (int size = 2; size <= n; size <<= 1) {
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int q = tid; q < (n >> 1); q += nt) {
+          const int lo = 2 * stride * (q / stride) + (q % stride), hi = lo + stride;
+          const bool up = (lo & size) == 0;
+          const uint64_t kl = key[lo], kh = key[hi];
+          const uint32_t il = idx[lo], ih = idx[hi];
+          if (entry_before(kh, ih, kl, il) == up) {
+            key[lo] = kh;
+            key[hi] = kl;
+            idx[lo] = ih;
+            idx[hi] = il;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int64_t j = tid; j < p.k; j += nt) {
+      const uint32_t s = idx[j];
+      const int64_t o = (row * p.k + j) * p.inner + in0;
+      values[o] = src[static_cast<int64_t>(s) * p.inner];
+      indices[o] = static_cast<int64_t>(s);
+    }
+    __syncthreads();  // LDS is reused by the next slice
+  }
+}
+
+template <typename T>
+hipError_t launch_typed(const void* in, void* values, int64_t* indices, const TopKArgs& p, hipStream_t stream) {
+  int n = 1;
+  while (n < p.dim) n <<= 1;
+  if (n < 2) n = 2;
+  const int threads = n / 2 < 64 ? 64 : (n / 2 > 1024 ? 1024 : n / 2);
+  const int64_t slices = p.rows * p.inner;
+  const unsigned grid = static_cast<unsigned>(slices < (int64_t{1} << 20) ? slices : (int64_t{1} << 20));
+  const size_t lds = static_cast<size_t>(n) * 12;
+  hipLaunchKernelGGL(topk_kernel<T>, dim3(grid), dim3(threads), lds, stream, static_cast<const T*>(in),
+                     static_cast<T*>(values), indices, p, n);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_topk(const void* in, int32_t elem_type, void* values, int64_t* indices, const TopKArgs& p,
+                       hipStream_t stream) {
+  if (p.rows * p.inner == 0 || p.k == 0) return hipSuccess;
+  switch (elem_type) {
+    case MOE_ELEM_FLOAT: return launch_typed<float>(in, values, indices, p, stream);
+    case MOE_ELEM_FLOAT16: return launch_typed<_Float16>(in, values, indices, p, stream);
+    case MOE_ELEM_BFLOAT16: return launch_typed<uint16_t>(in, values, indices, p, stream);
+    case MOE_ELEM_DOUBLE: return launch_typed<double>(in, values, indices, p, stream);
+    case MOE_ELEM_INT32: return launch_typed<int32_t>(in, values, indices, p, stream);
+    case MOE_ELEM_INT64: return launch_typed<int64_t>(in, values, indices, p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace moe

@@ -12,6 +12,7 @@ MOE_OK, MOE_FAIL, MOE_INVALID_ARGUMENT, MOE_NOT_IMPLEMENTED, MOE_EP_FAIL = 0, 1,
 STATUS_NAMES = {0: "OK", 1: "FAIL", 2: "INVALID_ARGUMENT", 9: "NOT_IMPLEMENTED", 11: "EP_FAIL"}
 
 ELEM_FLOAT, ELEM_UINT8, ELEM_FLOAT16, ELEM_BFLOAT16 = 1, 2, 10, 16
+ELEM_INT32, ELEM_INT64, ELEM_DOUBLE = 6, 7, 11
 ACTIVATIONS = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
 PATHS = {"auto": -1, "simt": 0, "decode": 1, "prefill": 2}
 
@@ -75,6 +76,22 @@ class MoeRouteParams(ctypes.Structure):
     ]
 
 
+class MoeTopKParams(ctypes.Structure):
+    _fields_ = [
+        ("input", ctypes.c_void_p),
+        ("elem_type", ctypes.c_int32),
+        ("largest", ctypes.c_int32),
+        ("sorted", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("dim", ctypes.c_int64),
+        ("inner", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("values", ctypes.c_void_p),
+        ("indices", ctypes.c_void_p),
+    ]
+
+
 # (name, restype, argtypes) of every function the header declares.
 EXPORTS = [
     ("moe_attributes_init", ctypes.c_int, [ctypes.POINTER(MoeAttributes), ctypes.c_char_p]),
@@ -100,6 +117,7 @@ EXPORTS = [
     ("moe_last_error", ctypes.c_char_p, []),
     ("moe_route_dispatch_scratch_size", ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     ("moe_route_dispatch_launch", ctypes.c_int, [ctypes.POINTER(MoeRouteParams), ctypes.c_void_p]),
+    ("moe_topk_launch", ctypes.c_int, [ctypes.POINTER(MoeTopKParams), ctypes.c_void_p]),
     ("moe_version", ctypes.c_char_p, []),
 ]
 

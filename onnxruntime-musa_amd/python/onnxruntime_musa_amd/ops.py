@@ -16,9 +16,9 @@ from typing import Optional, Sequence
 
 import torch
 
-from ._capi import (ACTIVATIONS, ELEM_BFLOAT16, ELEM_FLOAT, ELEM_FLOAT16, ELEM_UINT8, PATHS,
-                    MoeAttributes, MoeError, MoeRouteParams, MoeTensor, MoeWorkspaceLayout, check,
-                    load_library)
+from ._capi import (ACTIVATIONS, ELEM_BFLOAT16, ELEM_DOUBLE, ELEM_FLOAT, ELEM_FLOAT16, ELEM_INT32, ELEM_INT64,
+                    ELEM_UINT8, PATHS, MoeAttributes, MoeError, MoeRouteParams, MoeTensor, MoeTopKParams,
+                    MoeWorkspaceLayout, check, load_library)
 
 _ELEM = {torch.float32: ELEM_FLOAT, torch.float16: ELEM_FLOAT16, torch.bfloat16: ELEM_BFLOAT16,
          torch.uint8: ELEM_UINT8}
@@ -243,4 +243,43 @@ def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoi
     return res
 
 
-__all__ = ["MoE", "QMoE", "route_dispatch", "MoeError", "MOE_INPUTS", "QMOE_INPUTS"]
+_TOPK_ELEM = {torch.float32: ELEM_FLOAT, torch.float16: ELEM_FLOAT16, torch.bfloat16: ELEM_BFLOAT16,
+              torch.float64: ELEM_DOUBLE, torch.int32: ELEM_INT32, torch.int64: ELEM_INT64}
+
+
+def topk(x: torch.Tensor, k: int, axis: int = -1, largest: int = 1, sorted: int = 1,
+         stream: Optional[torch.cuda.Stream] = None):
+    """ONNX TopK (attributes axis, largest, sorted; K as a host integer, as
+    the reference binds it to CPU memory, musa/ep/src/kernels/math/topk.cc:163-177).
+    Returns (values, int64 indices) of shape x.shape with the axis cut to k."""
+    lib = load_library()
+    if x.dim() < 1:
+        raise ValueError("TopK input rank must be at least 1")
+    if not x.is_cuda or not x.is_contiguous():
+        raise ValueError("TopK input must be a contiguous GPU tensor")
+    ax = axis + x.dim() if axis < 0 else axis
+    if not 0 <= ax < x.dim():
+        raise ValueError("TopK axis out of range")
+    shape = list(x.shape)
+    rows = 1
+    for d in shape[:ax]:
+        rows *= d
+    inner = 1
+    for d in shape[ax + 1:]:
+        inner *= d
+    out_shape = shape[:ax] + [max(int(k), 0)] + shape[ax + 1:]
+    values = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+    indices = torch.empty(out_shape, dtype=torch.int64, device=x.device)
+    p = MoeTopKParams()
+    p.input = x.data_ptr() if x.numel() else None
+    p.elem_type = _TOPK_ELEM.get(x.dtype, 0)
+    p.largest, p.sorted = int(largest), int(sorted)
+    p.rows, p.dim, p.inner, p.k = rows, shape[ax], inner, int(k)
+    p.values = values.data_ptr() if values.numel() else None
+    p.indices = indices.data_ptr() if indices.numel() else None
+    s = stream if stream is not None else torch.cuda.current_stream(x.device)
+    check(lib.moe_topk_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
+    return values, indices
+
+
+__all__ = ["MoE", "QMoE", "route_dispatch", "topk", "MoeError", "MOE_INPUTS", "QMOE_INPUTS"]

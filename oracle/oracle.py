@@ -93,6 +93,31 @@ def route(logits: np.ndarray, k: int, normalize: bool = False, sigmoid: bool = F
     return ids, w
 
 
+def topk(x: np.ndarray, k: int, axis: int = -1, largest: int = 1):
+    """ONNX TopK restated: along `axis`, the k largest (or smallest) values
+    in sorted order, ties toward the lower index -- the reference's pair order
+    (musa/ep/src/kernels/math/topk_impl.mu:46-65: by value, then by index).
+    -0.0 and +0.0 compare equal.  Integers are compared exactly (no float
+    conversion).  Returns (values, int64 indices)."""
+    a = np.moveaxis(np.asarray(x), axis, -1)
+    lead = a.shape[:-1]
+    flat = a.reshape(-1, a.shape[-1])
+    d = flat.shape[1]
+    vals = np.empty((flat.shape[0], k), dtype=a.dtype)
+    idx = np.empty((flat.shape[0], k), dtype=np.int64)
+    for r in range(flat.shape[0]):
+        row = flat[r]
+        if np.issubdtype(row.dtype, np.integer):
+            key = [int(v) for v in row]
+        else:
+            key = [float(v) + 0.0 for v in row]  # -0.0 -> +0.0
+        order = sorted(range(d), key=(lambda i: (-key[i], i)) if largest else (lambda i: (key[i], i)))[:k]
+        idx[r] = order
+        vals[r] = row[order]
+    out_shape = lead + (k,)
+    return (np.moveaxis(vals.reshape(out_shape), -1, axis), np.moveaxis(idx.reshape(out_shape), -1, axis))
+
+
 def dispatch(ids: np.ndarray, E: int):
     """ids [T, k] -> (offsets [E+1], perm [T*k])."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -357,3 +357,28 @@ def test_prepack_rejects_small_buffer(lib, qkernel):
                                 ctypes.byref(flag))
     assert st == C.MOE_INVALID_ARGUMENT and flag.value == 0
     assert b"too small" in lib.moe_last_error()
+
+
+# ---- moe_topk_launch validation (returns before any launch) ----
+def topk_status(lib, **kw):
+    p = C.MoeTopKParams()
+    p.input, p.values, p.indices = FAKE, FAKE, FAKE
+    p.elem_type, p.largest, p.sorted = C.ELEM_FLOAT, 1, 1
+    p.rows, p.dim, p.inner, p.k = 2, 16, 1, 4
+    for key, val in kw.items():
+        setattr(p, key, val)
+    return lib.moe_topk_launch(ctypes.byref(p), None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(k=17), C.MOE_INVALID_ARGUMENT),          # k > dim (musa/ep/src/kernels/math/topk.cc:174-177)
+    (dict(k=-1), C.MOE_INVALID_ARGUMENT),
+    (dict(largest=2), C.MOE_INVALID_ARGUMENT),     # topk.cc:143-150
+    (dict(sorted=3), C.MOE_INVALID_ARGUMENT),
+    (dict(elem_type=C.ELEM_UINT8), C.MOE_NOT_IMPLEMENTED),  # topk.cc:179-183
+    (dict(dim=8193, k=3), C.MOE_NOT_IMPLEMENTED),  # one workgroup sorts a slice in LDS
+    (dict(k=0), C.MOE_OK),                         # empty output: nothing to launch
+    (dict(rows=0), C.MOE_OK),
+])
+def test_topk_validation(lib, kw, code):
+    assert topk_status(lib, **kw) == code

@@ -1,0 +1,134 @@
+"""ONNX TopK on the GPU against the oracle restatement.
+
+The cases restate the reference's own TopK tests (test/ops/test_topk.py):
+shapes, dtypes, axes, k values and the seeded or hand-written inputs listed
+there, compared exactly (values are copies of input elements, indices are
+integers).  Random cases with many ties cover the ordering rule (value, then
+lower index) over every dtype and up to the 8192-element axis limit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from onnxruntime_musa_amd import MoeError, topk
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def run(cuda, x: np.ndarray, k: int, axis=-1, largest=1, torch_dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(x))
+    if torch_dtype is not None:
+        t = t.to(torch_dtype)
+    t = t.to(cuda)
+    v, i = topk(t, k, axis=axis, largest=largest)
+    torch.cuda.synchronize()
+    host = t.cpu()
+    ref_in = host.float().numpy() if torch_dtype in (torch.float16, torch.bfloat16) else host.numpy()
+    ev, ei = oracle.topk(ref_in, k, axis=axis, largest=largest)
+    np.testing.assert_array_equal(i.cpu().numpy(), ei)
+    gv = v.cpu()
+    gv = gv.float().numpy() if torch_dtype in (torch.float16, torch.bfloat16) else gv.numpy()
+    np.testing.assert_array_equal(gv, ev)
+    return gv, i.cpu().numpy()
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16, np.float64, np.int32, np.int64])
+def test_largest_axis_last(cuda, dt):  # test_topk.py:20-45
+    x = np.array([[[1, 5, 3, 2], [4, 4, 7, 0]], [[9, 8, 8, 1], [3, 6, 2, 5]]], dtype=dt)
+    run(cuda, x, 2)
+
+
+def test_reference_cases(cuda):
+    # :48-62 smallest along axis 1
+    x = np.random.default_rng(0).standard_normal((3, 7, 5)).astype(np.float32)
+    run(cuda, x, 3, axis=1, largest=0)
+    # :95-126 real token-merger row, smallest, k = dim
+    row = np.array([[0.0, 1.0, 9.8013570e06, 1.0715436e07, 1.0715513e07, 1.0715654e07, 1.0819043e07,
+                     1.0823217e07, 0.0, 1.0, 0.0, 1.0715497e07, 1.0715646e07, 1.0849186e07]], dtype=np.float32)
+    run(cuda, row, 14, largest=0)
+    # :129-141 int64, dim 1024, k 512
+    run(cuda, np.random.default_rng(20260710).integers(-10000, 10000, size=(2, 1024), dtype=np.int64), 512)
+    # :144-155 int64 smallest with ties
+    run(cuda, np.array([[5, -1, -1, 9, 0, -3, -3, 7]], dtype=np.int64), 4, largest=0)
+    # :178-192 int64 dim 1300
+    run(cuda, np.random.default_rng(3).integers(-2000, 2000, size=(1, 1300), dtype=np.int64), 7)
+    # :195-209 integers above 2^53
+    v, i = run(cuda, np.array([[2**53, 2**53 + 1, 2**53 + 2, 0]], dtype=np.int64), 2)
+    np.testing.assert_array_equal(i, [[2, 1]])
+    # :212-227 adjacent floats
+    nxt = np.nextafter(np.float32(10.0), np.float32(np.inf))
+    v, i = run(cuda, np.array([[10.0, nxt, 9.0]], dtype=np.float32), 1)
+    assert i[0, 0] == 1
+    # :230-246 k = 1 on a non-last axis, smallest
+    v, i = run(cuda, np.array([[[4.0, 7.0], [1.0, 7.0], [1.0, 8.0], [3.0, 9.0]]], dtype=np.float32), 1, axis=1,
+               largest=0)
+    np.testing.assert_array_equal(i, [[[1, 0]]])
+    # :249-262 double, dim 1300, two equal maxima
+    x = np.random.default_rng(20260721).uniform(-4.0, 4.0, size=(2, 1300))
+    x[:, 31] = 20.0
+    x[:, 877] = 20.0
+    run(cuda, x, 11)
+
+
+@pytest.mark.parametrize("largest", [0, 1])
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64])
+def test_large_k(cuda, largest, dt):  # :265-289 permutation of 1300, k 1100
+    x = np.random.default_rng(7).permutation(np.arange(1300)).astype(dt)[None, :]
+    run(cuda, x, 1100, largest=largest)
+
+
+@pytest.mark.parametrize("largest", [0, 1])
+def test_ties(cuda, largest):
+    run(cuda, np.full((1, 4000), 3.25, dtype=np.float32), 128, largest=largest)  # :307-323
+    pattern = np.array([-3.0, -2.0, -1.0, 0.0, 1.0, 2.0, 3.0, 3.0])  # :326-340
+    run(cuda, np.tile(pattern, 500).astype(np.float32)[None, :], 128, largest=largest)
+    x = np.array([[5.0, 5.0, 5.0, 4.0, 4.0, 1.0, 0.0, -1.0, -1.0, -2.0, -2.0, -3.0],
+                  [2.0, -4.0, 2.0, -4.0, 3.0, 3.0, 0.0, 0.0, 1.0, 1.0, -1.0, -1.0]], dtype=np.float32)
+    run(cuda, x, 4, largest=largest)  # :360-395 (sorted output is a valid sorted=0 answer)
+    run(cuda, np.array([[0.0, -0.0, 1.0, -0.0]], dtype=np.float32), 3, largest=largest)
+
+
+@pytest.mark.parametrize("axis", [1, -2])
+@pytest.mark.parametrize("k", [1, 3])
+def test_axis_ties(cuda, axis, k):  # :343-357
+    run(cuda, ((np.arange(40).reshape(2, 5, 4) % 7) - 3).astype(np.float32), k, axis=axis)
+
+
+@pytest.mark.parametrize("shape,axis,k,dt", [
+    ((1, 3999), -1, 128, np.float32), ((1, 4000), -1, 127, np.float32),
+    ((1, 4000, 2), 1, 128, np.float32), ((1, 4000), -1, 128, np.float64),  # :398-421
+])
+def test_boundary_matrix(cuda, shape, axis, k, dt):
+    run(cuda, np.random.default_rng(20260720).integers(-16, 17, size=shape).astype(dt), k, axis=axis)
+
+
+@pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
+def test_half_types(cuda, tdt):
+    x = np.random.default_rng(5).integers(-50, 50, size=(64, 300)).astype(np.float32) / 8.0
+    run(cuda, x, 17, torch_dtype=tdt)
+    run(cuda, x, 300, largest=0, torch_dtype=tdt)
+
+
+@pytest.mark.parametrize("dim", [1, 2, 63, 64, 65, 1000, 8192])
+def test_dims_up_to_limit(cuda, dim):
+    x = np.random.default_rng(dim).integers(-20, 20, size=(5, dim, 3)).astype(np.float32)
+    run(cuda, x, min(dim, 9), axis=1)
+    run(cuda, x, dim, axis=1, largest=0)
+
+
+def test_many_rows_router_shape(cuda):
+    x = np.random.default_rng(1).standard_normal((8192, 128)).astype(np.float32)
+    run(cuda, x, 8)
+
+
+def test_k_zero_and_errors(cuda):
+    x = torch.ones((2, 3), device=cuda)
+    v, i = topk(x, 0)
+    assert v.shape == (2, 0) and i.shape == (2, 0)
+    with pytest.raises(MoeError) as ei:
+        topk(x, 4)
+    assert ei.value.code == 2
+    with pytest.raises(MoeError) as ei:
+        topk(torch.ones((1, 8193), device=cuda), 2)
+    assert ei.value.code == 9

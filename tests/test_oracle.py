@@ -456,3 +456,49 @@ def test_golden_qmoe_fixtures(fixture):
     r = oracle.forward_problem(cfg, h)
     np.testing.assert_array_equal(r["topk_ids"], fx["topk_ids"])
     np.testing.assert_allclose(r["out_f32"], fx["out"], rtol=0, atol=1e-6)
+
+
+# ---- TopK restatement (oracle.topk), pinned by the known answers the
+# reference's TopK tests state (test/ops/test_topk.py) ----
+def test_topk_oracle_reference_known_answers():
+    # :195-209 integers above 2^53 are ordered exactly
+    v, i = oracle.topk(np.array([[2**53, 2**53 + 1, 2**53 + 2, 0]], dtype=np.int64), 2)
+    np.testing.assert_array_equal(v, [[2**53 + 2, 2**53 + 1]])
+    np.testing.assert_array_equal(i, [[2, 1]])
+    # :212-227 adjacent float32 values are not ties
+    nxt = np.nextafter(np.float32(10.0), np.float32(np.inf))
+    v, i = oracle.topk(np.array([[10.0, nxt, 9.0]], dtype=np.float32), 1)
+    assert v[0, 0] == nxt and i[0, 0] == 1
+    # :230-246 k = 1 along a non-last axis, smallest, ties -> lower index
+    x = np.array([[[4.0, 7.0], [1.0, 7.0], [1.0, 8.0], [3.0, 9.0]]], dtype=np.float32)
+    v, i = oracle.topk(x, 1, axis=1, largest=0)
+    np.testing.assert_array_equal(v, [[[1.0, 7.0]]])
+    np.testing.assert_array_equal(i, [[[1, 0]]])
+    # :307-323 all equal -> arange(k), both directions
+    for largest in (0, 1):
+        v, i = oracle.topk(np.full((1, 4000), 3.25, dtype=np.float32), 128, largest=largest)
+        np.testing.assert_array_equal(i, np.arange(128)[None, :])
+    # :291-304 k = 0 gives empty outputs
+    v, i = oracle.topk(np.array([[3.0, 1.0, 2.0], [6.0, 5.0, 4.0]], dtype=np.float32), 0)
+    assert v.shape == (2, 0) and i.shape == (2, 0)
+
+
+def test_topk_oracle_against_stable_sort_and_brute_force():
+    rng = np.random.default_rng(3)
+    for trial in range(20):
+        d = int(rng.integers(1, 40))
+        x = rng.integers(-4, 5, size=(3, d)).astype(np.float32)  # many ties
+        k = int(rng.integers(0, d + 1))
+        for largest in (0, 1):
+            v, i = oracle.topk(x, k, largest=largest)
+            key = -x if largest else x
+            order = np.argsort(key, axis=-1, kind="stable")[:, :k]
+            np.testing.assert_array_equal(i, order)
+            np.testing.assert_array_equal(v, np.take_along_axis(x, order, axis=-1))
+    # -0.0 ties with +0.0 (value comparison): the lower index comes first
+    v, i = oracle.topk(np.array([[0.0, -0.0, 0.0]], dtype=np.float32), 3)
+    np.testing.assert_array_equal(i, [[0, 1, 2]])
+    # a planted mistake (ties toward the higher index) is caught
+    x = np.array([[1.0, 2.0, 2.0, 0.0]], dtype=np.float32)
+    _, i = oracle.topk(x, 1)
+    assert i[0, 0] == 1 and i[0, 0] != 2
