@@ -258,6 +258,23 @@ typedef struct moe_topk_params {
 } moe_topk_params;
 MOE_API moe_status moe_topk_launch(const moe_topk_params *params, void *stream);
 
+/* ONNX Softmax (opset 13 semantics: one axis), the router's normalisation
+ * as a stand-alone op: y = exp(x - max) / sum exp(x - max) along the axis of
+ * the input viewed as [outer, dim, inner], accumulated in fp32 (fp64 for
+ * double).  Types: float, float16, bfloat16, double.  Replaces the
+ * reference's LaunchMusaSoftmaxKernel(input, output, outer, dim, inner,
+ * elem_type, stream) (musa/ep/src/kernels/math/softmax_impl.h:5-8); an
+ * unsupported type -> MOE_NOT_IMPLEMENTED, a negative size ->
+ * MOE_INVALID_ARGUMENT. */
+typedef struct moe_softmax_params {
+  const void *input;
+  void *output;
+  int32_t elem_type; /* moe_elem_type */
+  int32_t pad_;
+  int64_t outer, dim, inner;
+} moe_softmax_params;
+MOE_API moe_status moe_softmax_launch(const moe_softmax_params *params, void *stream);
+
 /* Library version string. */
 MOE_API const char *moe_version(void);
 

@@ -95,6 +95,10 @@ constexpr int64_t kTopKMaxDim = 8192;  // one workgroup sorts a slice in LDS
 hipError_t launch_topk(const void* in, int32_t elem_type, void* values, int64_t* indices, const TopKArgs& p,
                        hipStream_t stream);
 
+// ONNX Softmax along the middle axis of [outer, dim, inner] (moe_softmax.hip).
+hipError_t launch_softmax(const void* in, void* out, int32_t elem_type, int64_t outer, int64_t dim, int64_t inner,
+                          hipStream_t stream);
+
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
                           hipStream_t stream);
 

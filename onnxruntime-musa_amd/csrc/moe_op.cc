@@ -718,6 +718,25 @@ moe_status moe_topk_launch(const moe_topk_params* p, void* stream) {
   }
 }
 
+moe_status moe_softmax_launch(const moe_softmax_params* p, void* stream) {
+  try {
+    if (!p) return fail(MOE_INVALID_ARGUMENT, "null params");
+    if (p->outer < 0 || p->dim < 0 || p->inner < 0) return fail(MOE_INVALID_ARGUMENT, "negative shape");
+    switch (p->elem_type) {
+      case MOE_ELEM_FLOAT: case MOE_ELEM_FLOAT16: case MOE_ELEM_BFLOAT16: case MOE_ELEM_DOUBLE: break;
+      default: return fail(MOE_NOT_IMPLEMENTED, "Softmax unsupported dtype");
+    }
+    if (p->outer * p->dim * p->inner == 0) return MOE_OK;
+    if (!p->input || !p->output) return fail(MOE_INVALID_ARGUMENT, "null tensor");
+    const hipError_t e = moe::launch_softmax(p->input, p->output, p->elem_type, p->outer, p->dim, p->inner,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "Softmax launch");
+    return MOE_OK;
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
+}
+
 moe_status moe_route_dispatch_launch(const moe_route_params* params, void* stream) {
   if (!params) return fail(MOE_INVALID_ARGUMENT, "null params");
   const moe_route_params& p = *params;

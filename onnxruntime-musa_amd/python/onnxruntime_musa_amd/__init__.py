@@ -12,7 +12,7 @@ Every call runs the hand-written HIP kernels of lib/libmoe_mi355x.so; there is
 no CPU or PyTorch fallback.  A missing library raises at import of the op.
 """
 from ._capi import get_library_path, load_library, MoeError  # noqa: F401
-from .ops import MoE, QMoE, route_dispatch, topk  # noqa: F401
+from .ops import MoE, QMoE, route_dispatch, softmax, topk  # noqa: F401
 
 EP_NAME = "MI355XExecutionProvider"
 

@@ -92,6 +92,18 @@ class MoeTopKParams(ctypes.Structure):
     ]
 
 
+class MoeSoftmaxParams(ctypes.Structure):
+    _fields_ = [
+        ("input", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+        ("elem_type", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
+        ("outer", ctypes.c_int64),
+        ("dim", ctypes.c_int64),
+        ("inner", ctypes.c_int64),
+    ]
+
+
 # (name, restype, argtypes) of every function the header declares.
 EXPORTS = [
     ("moe_attributes_init", ctypes.c_int, [ctypes.POINTER(MoeAttributes), ctypes.c_char_p]),
@@ -118,6 +130,7 @@ EXPORTS = [
     ("moe_route_dispatch_scratch_size", ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     ("moe_route_dispatch_launch", ctypes.c_int, [ctypes.POINTER(MoeRouteParams), ctypes.c_void_p]),
     ("moe_topk_launch", ctypes.c_int, [ctypes.POINTER(MoeTopKParams), ctypes.c_void_p]),
+    ("moe_softmax_launch", ctypes.c_int, [ctypes.POINTER(MoeSoftmaxParams), ctypes.c_void_p]),
     ("moe_version", ctypes.c_char_p, []),
 ]
 

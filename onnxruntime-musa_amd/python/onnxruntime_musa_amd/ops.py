@@ -17,8 +17,8 @@ from typing import Optional, Sequence
 import torch
 
 from ._capi import (ACTIVATIONS, ELEM_BFLOAT16, ELEM_DOUBLE, ELEM_FLOAT, ELEM_FLOAT16, ELEM_INT32, ELEM_INT64,
-                    ELEM_UINT8, PATHS, MoeAttributes, MoeError, MoeRouteParams, MoeTensor, MoeTopKParams,
-                    MoeWorkspaceLayout, check, load_library)
+                    ELEM_UINT8, PATHS, MoeAttributes, MoeError, MoeRouteParams, MoeSoftmaxParams, MoeTensor,
+                    MoeTopKParams, MoeWorkspaceLayout, check, load_library)
 
 _ELEM = {torch.float32: ELEM_FLOAT, torch.float16: ELEM_FLOAT16, torch.bfloat16: ELEM_BFLOAT16,
          torch.uint8: ELEM_UINT8}
@@ -282,4 +282,32 @@ def topk(x: torch.Tensor, k: int, axis: int = -1, largest: int = 1, sorted: int 
     return values, indices
 
 
-__all__ = ["MoE", "QMoE", "route_dispatch", "topk", "MoeError", "MOE_INPUTS", "QMOE_INPUTS"]
+def softmax(x: torch.Tensor, axis: int = -1, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+    """ONNX Softmax (opset 13: along one axis, default -1) for float,
+    float16, bfloat16 and double."""
+    lib = load_library()
+    if not x.is_cuda or not x.is_contiguous():
+        raise ValueError("Softmax input must be a contiguous GPU tensor")
+    if x.dim() == 0:
+        raise ValueError("Softmax input rank must be at least 1")
+    ax = axis + x.dim() if axis < 0 else axis
+    if not 0 <= ax < x.dim():
+        raise ValueError("Softmax axis out of range")
+    outer = 1
+    for d in x.shape[:ax]:
+        outer *= d
+    inner = 1
+    for d in x.shape[ax + 1:]:
+        inner *= d
+    y = torch.empty_like(x)
+    p = MoeSoftmaxParams()
+    p.input = x.data_ptr() if x.numel() else None
+    p.output = y.data_ptr() if y.numel() else None
+    p.elem_type = _TOPK_ELEM.get(x.dtype, 0) if x.dtype.is_floating_point else 0
+    p.outer, p.dim, p.inner = outer, x.shape[ax], inner
+    s = stream if stream is not None else torch.cuda.current_stream(x.device)
+    check(lib.moe_softmax_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
+    return y
+
+
+__all__ = ["MoE", "QMoE", "route_dispatch", "topk", "softmax", "MoeError", "MOE_INPUTS", "QMOE_INPUTS"]

@@ -118,6 +118,16 @@ def topk(x: np.ndarray, k: int, axis: int = -1, largest: int = 1):
     return (np.moveaxis(vals.reshape(out_shape), -1, axis), np.moveaxis(idx.reshape(out_shape), -1, axis))
 
 
+def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
+    """ONNX Softmax restated in float64: exp(x - max) * (1 / sum exp(x - max))
+    along `axis` (musa/ep/src/kernels/math/softmax_impl.mu:49-84 computes
+    the same steps in fp32, or fp64 for double)."""
+    a = np.asarray(x, dtype=np.float64)
+    m = np.max(a, axis=axis, keepdims=True)
+    e = np.exp(a - m)
+    return e * (1.0 / np.sum(e, axis=axis, keepdims=True))
+
+
 def dispatch(ids: np.ndarray, E: int):
     """ids [T, k] -> (offsets [E+1], perm [T*k])."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)

@@ -382,3 +382,17 @@ def topk_status(lib, **kw):
 ])
 def test_topk_validation(lib, kw, code):
     assert topk_status(lib, **kw) == code
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(elem_type=C.ELEM_INT32), C.MOE_NOT_IMPLEMENTED),
+    (dict(dim=-1), C.MOE_INVALID_ARGUMENT),
+    (dict(outer=0), C.MOE_OK),
+])
+def test_softmax_validation(lib, kw, code):
+    p = C.MoeSoftmaxParams()
+    p.input, p.output, p.elem_type = FAKE, FAKE, C.ELEM_FLOAT
+    p.outer, p.dim, p.inner = 4, 8, 1
+    for key, val in kw.items():
+        setattr(p, key, val)
+    assert lib.moe_softmax_launch(ctypes.byref(p), None) == code

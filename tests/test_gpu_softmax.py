@@ -1,0 +1,50 @@
+"""ONNX Softmax on the GPU against the float64 oracle.
+
+The cases restate the reference's Softmax tests (test/ops/test_softmax.py):
+shapes, axes, dtypes and seeds, with its tolerances (fp32 1e-5 relative /
+1e-6 absolute as the CPU-vs-device default of op_test_utils, fp16 and bf16
+2e-2, double 1e-6 / 1e-7), plus long rows, strided axes and the router's
+shape.
+"""
+import numpy as np
+import pytest
+import torch
+
+from onnxruntime_musa_amd import softmax
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-5, 1e-6), torch.float16: (2e-2, 2e-2), torch.bfloat16: (2e-2, 2e-2),
+       torch.float64: (1e-6, 1e-7)}
+
+
+def run(cuda, x: np.ndarray, axis=-1, dt=torch.float32):
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(dt).to(cuda)
+    y = softmax(t, axis)
+    torch.cuda.synchronize()
+    ref = oracle.softmax(t.cpu().double().numpy(), axis)
+    rtol, atol = TOL[dt]
+    np.testing.assert_allclose(y.cpu().double().numpy(), ref, rtol=rtol, atol=atol)
+
+
+def test_reference_cases(cuda):
+    run(cuda, np.random.default_rng(0).standard_normal((16, 32)), -1)      # :14-22
+    run(cuda, np.random.default_rng(1).standard_normal((16, 32)), 0)       # :25-33
+    run(cuda, np.random.default_rng(2).standard_normal((2, 5, 4)), 1)      # :36-44
+    run(cuda, np.random.default_rng(3).standard_normal((32,)))             # :47-49
+    run(cuda, np.random.default_rng(4).standard_normal((8, 16)), -1, torch.float16)   # :52-62
+    run(cuda, np.random.default_rng(5).standard_normal((8, 16)), -1, torch.float64)   # :65-75
+    run(cuda, np.random.default_rng(6).standard_normal((4, 8)), -1, torch.bfloat16)   # :78-112
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("shape,axis", [((3, 1000), -1), ((7, 4097), 1), ((5, 6, 33), 1), ((2, 300, 4), 0),
+                                        ((8192, 128), -1), ((1, 1), 0)])
+def test_shapes(cuda, dt, shape, axis):
+    run(cuda, 3.0 * np.random.default_rng(sum(shape)).standard_normal(shape), axis, dt)
+
+
+def test_large_values_are_shift_invariant(cuda):
+    x = np.random.default_rng(9).standard_normal((4, 64)) + 80.0
+    run(cuda, x, -1)

@@ -502,3 +502,24 @@ def test_topk_oracle_against_stable_sort_and_brute_force():
     x = np.array([[1.0, 2.0, 2.0, 0.0]], dtype=np.float32)
     _, i = oracle.topk(x, 1)
     assert i[0, 0] == 1 and i[0, 0] != 2
+
+
+def test_softmax_oracle_closed_forms():
+    # rows sum to one; uniform rows give 1/dim; shift invariance; two-element
+    # softmax is the logistic function of the difference
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((5, 7, 3))
+    for axis in (0, 1, 2, -1):
+        y = oracle.softmax(x, axis)
+        np.testing.assert_allclose(np.sum(y, axis=axis), 1.0, rtol=1e-12)
+        np.testing.assert_allclose(oracle.softmax(x + 123.0, axis), y, rtol=1e-12)
+    np.testing.assert_allclose(oracle.softmax(np.zeros((2, 8)), -1), 1.0 / 8)
+    a, b = 0.7, -1.9
+    y = oracle.softmax(np.array([[a, b]]), -1)
+    np.testing.assert_allclose(y[0, 0], 1.0 / (1.0 + np.exp(b - a)), rtol=1e-14)
+    # the router's softmax (the C oracle) on the same logits agrees
+    lg = rng.standard_normal((6, 8)).astype(np.float32)
+    _, w = oracle.route(lg, 8, False, False)
+    ids, _ = oracle.route(lg, 8, False, False)
+    np.testing.assert_allclose(w, np.take_along_axis(oracle.softmax(lg.astype(np.float64), -1), ids, axis=-1),
+                               rtol=1e-5)
