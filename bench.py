@@ -156,6 +156,60 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
     return res, None
 
 
+def run_op(spec: str, steps: int, warmup: int, dev) -> dict:
+    """Times the stand-alone TopK or Softmax op on an fp32 [rows, dim] input
+    along the last axis.  Algorithmic bytes: the input read once plus the
+    outputs written once (TopK: k values and k int64 indices per row)."""
+    import ctypes
+
+    import torch
+
+    from onnxruntime_musa_amd import _capi as C
+
+    parts = spec.split(":")
+    op = parts[0]
+    rows, dim = (int(v) for v in parts[1].split("x"))
+    k = int(parts[2]) if len(parts) > 2 else 8
+    x = torch.randn((rows, dim), device=dev)
+    lib = C.load_library()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    # buffers and parameters built once, so that the loop times the kernels
+    # and not the Python wrapper's allocations
+    if op == "topk":
+        vals = torch.empty((rows, k), device=dev)
+        idx = torch.empty((rows, k), dtype=torch.int64, device=dev)
+        prm = C.MoeTopKParams(input=x.data_ptr(), elem_type=C.ELEM_FLOAT, largest=1, sorted=1, rows=rows, dim=dim,
+                              inner=1, k=k, values=vals.data_ptr(), indices=idx.data_ptr())
+        fn = lib.moe_topk_launch
+        nbytes = rows * dim * 4 + rows * k * (4 + 8)
+    elif op == "softmax":
+        y = torch.empty_like(x)
+        prm = C.MoeSoftmaxParams(input=x.data_ptr(), output=y.data_ptr(), elem_type=C.ELEM_FLOAT, outer=rows,
+                                 dim=dim, inner=1)
+        fn = lib.moe_softmax_launch
+        nbytes = rows * dim * 4 * 2
+    else:
+        raise SystemExit(f"unknown op {op}")
+    ref = ctypes.byref(prm)
+
+    def call():
+        C.check(fn(ref, stream))
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        call()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return dict(op=op, rows=rows, dim=dim, k=k if op == "topk" else None, dtype="f32", ms_per_call=round(ms, 4),
+                roofline=dict(bound="hbm", achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                              frac=round(gbs / PEAK_HBM_GBS, 4)))
+
+
 def cpu_baseline(prob, budget_s: float = 12.0):
     """Times the oracle on the headline workload on this host's cores."""
     import numpy as np
@@ -188,6 +242,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", default=None, help="name:tokens to run instead of the headline")
     ap.add_argument("--no-prepack", action="store_true", help="keep the expert weights in the op's row-major layout")
+    ap.add_argument("--op", default=None, metavar="OP:ROWSxDIM[:K]",
+                    help="time the stand-alone topk or softmax op on a [rows, dim] fp32 input instead "
+                         "(e.g. topk:8192x128:8, softmax:8192x4096)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -208,6 +265,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": n, "copies": args.steps}), flush=True)
+        return
+    if args.op:
+        print(json.dumps(run_op(args.op, args.steps, args.warmup, dev)), flush=True)
         return
     name, T = HEADLINE
     if args.workload:

@@ -2,7 +2,9 @@
 // router's ordering rule: values by key, ties toward the lower index
 // (musa/ep/src/kernels/math/topk_impl.mu:46-65).
 //
-// One workgroup per (row, inner) slice of the input viewed as [rows, dim,
+// Axes up to 512 with k <= 32: one wavefront per slice, k rounds of a wave
+// arg-max over keys held in registers (topk_wave_kernel).  Otherwise one
+// workgroup per (row, inner) slice of the input viewed as [rows, dim,
 // inner].  The slice's dim elements become order-preserving integer keys in
 // LDS (floats: sign-magnitude bits flipped to two's-complement order, -0.0
 // folded onto +0.0 so that it ties with +0.0 as a value comparison does;
@@ -103,13 +105,87 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
   }
 }
 
+// Short axes and small k: one wavefront per slice.  Each lane keeps up to
+// kWaveVpl (key, index) entries in registers; k rounds of a wave arg-max
+// under the same order (key desc, index asc) pick the outputs in sorted
+// order -- no LDS, no barriers.
+constexpr int kWaveVpl = 8;
+constexpr int kWaveMaxK = 32;
+
+template <typename T, int VPL>
+__global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in, T* __restrict__ values,
+                                                        int64_t* __restrict__ indices, TopKArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = blockDim.x / kWave;
+  const int64_t slices = p.rows * p.inner;
+  const int dim = static_cast<int>(p.dim), k = static_cast<int>(p.k);
+  for (int64_t sl = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; sl < slices;
+       sl += static_cast<int64_t>(gridDim.x) * wpb) {
+    const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
+    const T* src = in + row * p.dim * p.inner + in0;
+    uint64_t key[VPL];
+    bool live[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int i = lane + kWave * v;
+      live[v] = i < dim;
+      const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
+      key[v] = p.largest ? kv : ~kv;
+    }
+    for (int j = 0; j < k; ++j) {
+      uint64_t bk = 0;
+      uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const uint32_t i = static_cast<uint32_t>(lane + kWave * v);
+        if (live[v] && entry_before(key[v], i, bk, bi)) {
+          bk = key[v];
+          bi = i;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, kWave));
+        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, kWave));
+        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, kWave));
+        const uint64_t ok = (static_cast<uint64_t>(ohi) << 32) | olo;
+        if (entry_before(ok, oi, bk, bi)) {
+          bk = ok;
+          bi = oi;
+        }
+      }
+      // the owner of the winner retires it and writes the output
+      if (static_cast<int>(bi & 63) == lane) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+          if (v == static_cast<int>(bi >> 6)) live[v] = false;
+        const int64_t o = (row * p.k + j) * p.inner + in0;
+        values[o] = src[static_cast<int64_t>(bi) * p.inner];
+        indices[o] = static_cast<int64_t>(bi);
+      }
+    }
+  }
+}
+
 template <typename T>
 hipError_t launch_typed(const void* in, void* values, int64_t* indices, const TopKArgs& p, hipStream_t stream) {
+  const int64_t slices = p.rows * p.inner;
+  if (p.dim <= kWave * kWaveVpl && p.k <= kWaveMaxK) {
+    const int64_t blocks = (slices + 3) / 4;  // 4 waves per block
+    const dim3 grid(static_cast<unsigned>(blocks < (1 << 20) ? blocks : (1 << 20)));
+    const T* x = static_cast<const T*>(in);
+    T* v = static_cast<T*>(values);
+    // entries per lane: the power of two that covers dim
+    if (p.dim <= kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 1>), grid, dim3(256), 0, stream, x, v, indices, p);
+    else if (p.dim <= 2 * kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 2>), grid, dim3(256), 0, stream, x, v, indices, p);
+    else if (p.dim <= 4 * kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 4>), grid, dim3(256), 0, stream, x, v, indices, p);
+    else hipLaunchKernelGGL((topk_wave_kernel<T, kWaveVpl>), grid, dim3(256), 0, stream, x, v, indices, p);
+    return hipGetLastError();
+  }
   int n = 1;
   while (n < p.dim) n <<= 1;
   if (n < 2) n = 2;
   const int threads = n / 2 < 64 ? 64 : (n / 2 > 1024 ? 1024 : n / 2);
-  const int64_t slices = p.rows * p.inner;
   const unsigned grid = static_cast<unsigned>(slices < (int64_t{1} << 20) ? slices : (int64_t{1} << 20));
   const size_t lds = static_cast<size_t>(n) * 12;
   hipLaunchKernelGGL(topk_kernel<T>, dim3(grid), dim3(threads), lds, stream, static_cast<const T*>(in),
