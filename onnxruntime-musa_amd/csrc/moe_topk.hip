@@ -2,8 +2,9 @@
 // router's ordering rule: values by key, ties toward the lower index
 // (musa/ep/src/kernels/math/topk_impl.mu:46-65).
 //
-// Axes up to 512 with k <= 32: one wavefront per slice, k rounds of a wave
-// arg-max over keys held in registers (topk_wave_kernel).  Otherwise one
+// Axes up to 512 with k <= 32: lane groups of a wavefront take a slice each,
+// k rounds of a group arg-max over keys held in registers
+// (topk_wave_kernel).  Otherwise one
 // workgroup per (row, inner) slice of the input viewed as [rows, dim,
 // inner].  The slice's dim elements become order-preserving integer keys in
 // LDS (floats: sign-magnitude bits flipped to two's-complement order, -0.0
@@ -105,30 +106,34 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
   }
 }
 
-// Short axes and small k: one wavefront per slice.  Each lane keeps up to
-// kWaveVpl (key, index) entries in registers; k rounds of a wave arg-max
-// under the same order (key desc, index asc) pick the outputs in sorted
-// order -- no LDS, no barriers.
+// Short axes and small k: lane groups of G lanes take one slice each (64 / G
+// slices per wavefront), every lane holding kWaveVpl (key, index) entries
+// in registers; k rounds of a group arg-max (log2 G butterfly steps) under
+// the same order (key desc, index asc) pick the outputs in sorted order --
+// no LDS, no barriers.
 constexpr int kWaveVpl = 8;
 constexpr int kWaveMaxK = 32;
 
-template <typename T, int VPL>
+template <typename T, int G>
 __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in, T* __restrict__ values,
                                                         int64_t* __restrict__ indices, TopKArgs p) {
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, sub = lane % G;
+  constexpr int kPerWave = kWave / G;
   const int64_t wpb = blockDim.x / kWave;
   const int64_t slices = p.rows * p.inner;
   const int dim = static_cast<int>(p.dim), k = static_cast<int>(p.k);
-  for (int64_t sl = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; sl < slices;
-       sl += static_cast<int64_t>(gridDim.x) * wpb) {
-    const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
+  for (int64_t s0 = (static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave) * kPerWave; s0 < slices;
+       s0 += static_cast<int64_t>(gridDim.x) * wpb * kPerWave) {
+    const int64_t sl = s0 + lane / G;
+    const bool valid = sl < slices;
+    const int64_t row = valid ? sl / p.inner : 0, in0 = valid ? sl - row * p.inner : 0;
     const T* src = in + row * p.dim * p.inner + in0;
-    uint64_t key[VPL];
-    bool live[VPL];
+    uint64_t key[kWaveVpl];
+    bool live[kWaveVpl];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int i = lane + kWave * v;
-      live[v] = i < dim;
+    for (int v = 0; v < kWaveVpl; ++v) {
+      const int i = sub + G * v;
+      live[v] = valid && i < dim;
       const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
       key[v] = p.largest ? kv : ~kv;
     }
@@ -136,18 +141,18 @@ __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in
       uint64_t bk = 0;
       uint32_t bi = 0xFFFFFFFFu;
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const uint32_t i = static_cast<uint32_t>(lane + kWave * v);
+      for (int v = 0; v < kWaveVpl; ++v) {
+        const uint32_t i = static_cast<uint32_t>(sub + G * v);
         if (live[v] && entry_before(key[v], i, bk, bi)) {
           bk = key[v];
           bi = i;
         }
       }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, kWave));
-        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, kWave));
-        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, kWave));
+      for (int o = G / 2; o > 0; o >>= 1) {
+        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, G));
+        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, G));
+        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, G));
         const uint64_t ok = (static_cast<uint64_t>(ohi) << 32) | olo;
         if (entry_before(ok, oi, bk, bi)) {
           bk = ok;
@@ -155,10 +160,10 @@ __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in
         }
       }
       // the owner of the winner retires it and writes the output
-      if (static_cast<int>(bi & 63) == lane) {
+      if (valid && static_cast<int>(bi % G) == sub) {
 #pragma unroll
-        for (int v = 0; v < VPL; ++v)
-          if (v == static_cast<int>(bi >> 6)) live[v] = false;
+        for (int v = 0; v < kWaveVpl; ++v)
+          if (v == static_cast<int>(bi / G)) live[v] = false;
         const int64_t o = (row * p.k + j) * p.inner + in0;
         values[o] = src[static_cast<int64_t>(bi) * p.inner];
         indices[o] = static_cast<int64_t>(bi);
@@ -171,15 +176,21 @@ template <typename T>
 hipError_t launch_typed(const void* in, void* values, int64_t* indices, const TopKArgs& p, hipStream_t stream) {
   const int64_t slices = p.rows * p.inner;
   if (p.dim <= kWave * kWaveVpl && p.k <= kWaveMaxK) {
-    const int64_t blocks = (slices + 3) / 4;  // 4 waves per block
+    // lanes per slice: the power of two (4 .. 64) whose 8 entries per lane cover dim
+    const int g = p.dim <= 4 * kWaveVpl ? 4 : (p.dim <= 8 * kWaveVpl ? 8 : (p.dim <= 16 * kWaveVpl ? 16
+                : (p.dim <= 32 * kWaveVpl ? 32 : 64)));
+    const int64_t per_block = 4 * (kWave / g);  // 4 waves per block
+    const int64_t blocks = (slices + per_block - 1) / per_block;
     const dim3 grid(static_cast<unsigned>(blocks < (1 << 20) ? blocks : (1 << 20)));
     const T* x = static_cast<const T*>(in);
     T* v = static_cast<T*>(values);
-    // entries per lane: the power of two that covers dim
-    if (p.dim <= kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 1>), grid, dim3(256), 0, stream, x, v, indices, p);
-    else if (p.dim <= 2 * kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 2>), grid, dim3(256), 0, stream, x, v, indices, p);
-    else if (p.dim <= 4 * kWave) hipLaunchKernelGGL((topk_wave_kernel<T, 4>), grid, dim3(256), 0, stream, x, v, indices, p);
-    else hipLaunchKernelGGL((topk_wave_kernel<T, kWaveVpl>), grid, dim3(256), 0, stream, x, v, indices, p);
+    switch (g) {
+      case 4: hipLaunchKernelGGL((topk_wave_kernel<T, 4>), grid, dim3(256), 0, stream, x, v, indices, p); break;
+      case 8: hipLaunchKernelGGL((topk_wave_kernel<T, 8>), grid, dim3(256), 0, stream, x, v, indices, p); break;
+      case 16: hipLaunchKernelGGL((topk_wave_kernel<T, 16>), grid, dim3(256), 0, stream, x, v, indices, p); break;
+      case 32: hipLaunchKernelGGL((topk_wave_kernel<T, 32>), grid, dim3(256), 0, stream, x, v, indices, p); break;
+      default: hipLaunchKernelGGL((topk_wave_kernel<T, 64>), grid, dim3(256), 0, stream, x, v, indices, p); break;
+    }
     return hipGetLastError();
   }
   int n = 1;
