@@ -5,8 +5,11 @@
 // (musa/ep/src/kernels/math/softmax_impl.mu:49-84).
 //
 // The input is viewed as [outer, dim, inner].  With inner == 1 one wavefront
-// takes a row (lanes over dim: coalesced loads, butterfly max and sum);
-// otherwise one thread takes an (outer, inner) position and walks dim, so
+// takes a row.  For long rows each lane keeps a running maximum and a sum of
+// exponentials rescaled whenever its maximum rises, the lanes' pairs merge
+// in a butterfly, and a second pass writes -- two reads of the row instead of
+// three (max, sum, write), which short rows keep.
+// Otherwise one thread takes an (outer, inner) position and walks dim, so
 // that neighbouring threads read neighbouring inner elements.
 #include <stdint.h>
 
@@ -57,6 +60,11 @@ __device__ __forceinline__ A sm_wave_sum(A v) {
   return v;
 }
 
+// Rows at least this long take the online max-and-sum pass (16 elements per
+// lane or more); shorter ones spend less on a max pass, a sum pass and plain
+// butterflies than on the exponentials of the online merge.
+constexpr int64_t kOnlineDim = 1024;
+
 // inner == 1: one wavefront per row
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__ in, T* __restrict__ out,
@@ -66,15 +74,35 @@ __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__
   for (int64_t r = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; r < rows;
        r += static_cast<int64_t>(gridDim.x) * wpb) {
     const T* x = in + r * dim;
-    A m = -INFINITY;
-    for (int64_t d = lane; d < dim; d += kWave) {
-      const A v = sm_load<T, A>(x, d);
-      m = v > m ? v : m;
+    A m = -INFINITY, s = 0;
+    if (dim >= kOnlineDim) {
+      for (int64_t d = lane; d < dim; d += kWave) {
+        const A v = sm_load<T, A>(x, d);
+        if (v > m) {
+          s = s * sm_exp(m - v) + static_cast<A>(1);  // exp(-inf) = 0 on a lane's first element
+          m = v;
+        } else if (m != -INFINITY) {  // -inf elements before any finite one add nothing
+          s += sm_exp(v - m);
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const A om = __shfl_xor(m, o, kWave), os = __shfl_xor(s, o, kWave);
+        const A nm = om > m ? om : m;
+        // a side with nothing summed yet (s = 0, m = -inf) adds nothing
+        s = (m == nm ? s : (s == 0 ? static_cast<A>(0) : s * sm_exp(m - nm))) +
+            (om == nm ? os : (os == 0 ? static_cast<A>(0) : os * sm_exp(om - nm)));
+        m = nm;
+      }
+    } else {
+      for (int64_t d = lane; d < dim; d += kWave) {
+        const A v = sm_load<T, A>(x, d);
+        m = v > m ? v : m;
+      }
+      m = sm_wave_max(m);
+      for (int64_t d = lane; d < dim; d += kWave) s += sm_exp(sm_load<T, A>(x, d) - m);
+      s = sm_wave_sum(s);
     }
-    m = sm_wave_max(m);
-    A s = 0;
-    for (int64_t d = lane; d < dim; d += kWave) s += sm_exp(sm_load<T, A>(x, d) - m);
-    s = sm_wave_sum(s);
     const A inv = static_cast<A>(1) / s;
     for (int64_t d = lane; d < dim; d += kWave) sm_store<T, A>(out + r * dim, d, sm_exp(sm_load<T, A>(x, d) - m) * inv);
   }

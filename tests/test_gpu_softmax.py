@@ -48,3 +48,19 @@ def test_shapes(cuda, dt, shape, axis):
 def test_large_values_are_shift_invariant(cuda):
     x = np.random.default_rng(9).standard_normal((4, 64)) + 80.0
     run(cuda, x, -1)
+
+
+@pytest.mark.parametrize("dim", [200, 3000])
+def test_masked_rows(cuda, dim):
+    # -inf (masked) entries, some rows led by a masked prefix, one row all but one masked
+    x = np.random.default_rng(dim).standard_normal((6, dim)).astype(np.float32)
+    x[0, : dim // 2] = -np.inf
+    x[1, ::3] = -np.inf
+    x[2, :-1] = -np.inf
+    t = torch.from_numpy(x).to(cuda)
+    y = softmax(t, -1)
+    torch.cuda.synchronize()
+    ref = oracle.softmax(x.astype(np.float64), -1)
+    got = y.cpu().double().numpy()
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
