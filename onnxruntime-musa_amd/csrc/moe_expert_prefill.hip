@@ -222,17 +222,25 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       }
     }
   };
-  // wave-private window buffers: [2][64 lanes][16 bytes]
-  __shared__ __attribute__((aligned(16))) uint8_t sS[kFold ? 4 * 2 * 64 * 16 : 16];
-  uint8_t* const swave = sS + (kFold ? wave * 2 * 64 * 16 : 0);
+  // wave-private window buffers: [2][64 lanes][16 bytes], lanes 20 bytes
+  // apart: the 32 lanes that read one 2-byte scale each (lane lr reads lane
+  // j * 32 + lr's window) then fall on distinct banks (a 16-byte stride put
+  // 2 to 4 of them on one bank)
+  constexpr int kWin = 20;
+  __shared__ __attribute__((aligned(16))) uint8_t sS[kFold ? 4 * 2 * 64 * kWin : 16];
+  uint8_t* const swave = sS + (kFold ? wave * 2 * 64 * kWin : 0);
   auto sstore = [&](int m) {
-    if constexpr (kFold) *reinterpret_cast<u32x4_t*>(swave + ((m & 1) * 64 + lane) * 16) = swin;
+    if constexpr (kFold) {
+      uint32_t* d = reinterpret_cast<uint32_t*>(swave + ((m & 1) * 64 + lane) * kWin);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[q] = swin[q];
+    }
   };
   auto win_of = [&](int c) { return ((kbeg + c * BK) >> bshift) / WB; };  // window of stage c
   // scale of block j for block index b (this lane's row), 0 past K
   auto sread = [&](int j, int b) -> float {
     const typename ST::storage* ent =
-        reinterpret_cast<const typename ST::storage*>(swave + (((b / WB) & 1) * 64 + j * 32 + lr) * 16);
+        reinterpret_cast<const typename ST::storage*>(swave + (((b / WB) & 1) * 64 + j * 32 + lr) * kWin);
     const float v = to_f32<ST>(ent[b % WB]);
     return b < nblk ? v : 0.0f;
   };
