@@ -122,6 +122,61 @@ __device__ __forceinline__ int id_bits(int E) {
 // The logits are first copied to LDS with one load per element: when every
 // workgroup of a grid routes the same batch, a load per token and wave would
 // send thousands of requests for the same few cache lines to one L2 channel.
+// Routes tokens t0 + lane / G (G = the power of two >= E, E <= 64: 64 / G
+// tokens per wavefront) with the calling wavefront: the steps of route_token
+// with log2(G) butterfly steps instead of 6.  Lanes past E hold -inf / 0,
+// which the omitted steps of a full-wave butterfly would only have added or
+// compared, so the sums and the chosen experts are bit-identical to
+// route_token's.  Returns true in the lanes e = lane % G < k of tokens below
+// T, with *t the token, *id its e-th expert and *w the weight.
+template <typename LT>
+__device__ __forceinline__ bool route_group(const void* logits, int64_t t0, int64_t T, int E, int k, bool normalize,
+                                            bool sigm, int lane, int64_t* t, int* id, float* w) {
+  const int G = E <= 8 ? 8 : (E <= 16 ? 16 : (E <= 32 ? 32 : 64));
+  const int e = lane % G;
+  const int64_t tok = t0 + lane / G;
+  const bool valid = tok < T && e < E;
+  const float v = valid ? load_logit<LT>(logits, tok * E + e) : -INFINITY;
+  bool taken = !valid;
+  float m = v;
+  for (int o = G / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, G));
+  float sum = 0.0f;
+  if (!sigm) {
+    sum = valid ? expf(v - m) : 0.0f;
+    for (int o = G / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, G);
+  }
+  int my_id = 0;
+  float my_p = 0.0f, wsum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    float bv = taken ? -INFINITY : v;
+    int bid = taken ? INT_MAX : e;
+    for (int o = G / 2; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, G);
+      const int oid = __shfl_xor(bid, o, G);
+      if (cand_before(ov, oid, bv, bid)) {
+        bv = ov;
+        bid = oid;
+      }
+    }
+    if (e == bid) taken = true;
+    const float pj = sigm ? 1.0f / (1.0f + expf(-bv)) : expf(bv - m) / sum;
+    wsum += pj;
+    if (e == j) {
+      my_id = bid;
+      my_p = pj;
+    }
+  }
+  *t = tok;
+  *id = my_id;
+  *w = normalize ? my_p / wsum : my_p;
+  return tok < T && e < k;
+}
+
+// Tokens per wavefront of route_group.
+__device__ __forceinline__ int route_group_tokens(int E) {
+  return kWave / (E <= 8 ? 8 : (E <= 16 ? 16 : (E <= 32 ? 32 : 64)));
+}
+
 // LDS bytes route_dispatch_block needs as scratch.
 inline size_t route_block_scratch_bytes(int64_t T, int64_t E, int64_t k, int nwaves, int logit_bytes) {
   return static_cast<size_t>((2 * E + nwaves * E + T * k) * 4 + T * E * logit_bytes);
@@ -144,53 +199,18 @@ __device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* 
   for (int i = tid; i < T * E; i += blockDim.x) xl[i] = xg[i];
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  // Tokens in lane groups of G = the power of two >= E (64 / G tokens per
-  // wave): the same steps as route_token with log2(G) butterfly steps instead
-  // of 6.  Lanes past E hold -inf / 0, which the omitted steps of a full-wave
-  // butterfly would only have added or compared, so the sums and the chosen
-  // experts are bit-identical to route_token's.
-  const int G = E <= 8 ? 8 : (E <= 16 ? 16 : (E <= 32 ? 32 : 64));
-  const int tpw = kWave / G, e = lane % G;
-  const bool sigm = p.sigmoid != 0;
+  // tokens in lane groups (route_group)
+  const int tpw = route_group_tokens(E);
   for (int t0 = wave * tpw; t0 < T; t0 += nwaves * tpw) {
-    const int t = t0 + lane / G;
-    const bool valid = t < T && e < E;
-    const float v = valid ? load_logit<LT>(xl, static_cast<int64_t>(t) * E + e) : -INFINITY;
-    bool taken = !valid;
-    float m = v;
-    for (int o = G / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, G));
-    float sum = 0.0f;
-    if (!sigm) {
-      sum = valid ? expf(v - m) : 0.0f;
-      for (int o = G / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, G);
-    }
-    int my_id = 0;
-    float my_p = 0.0f, wsum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      float bv = taken ? -INFINITY : v;
-      int bid = taken ? INT_MAX : e;
-      for (int o = G / 2; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, G);
-        const int oid = __shfl_xor(bid, o, G);
-        if (cand_before(ov, oid, bv, bid)) {
-          bv = ov;
-          bid = oid;
-        }
-      }
-      if (e == bid) taken = true;
-      const float pj = sigm ? 1.0f / (1.0f + expf(-bv)) : expf(bv - m) / sum;
-      wsum += pj;
-      if (e == j) {
-        my_id = bid;
-        my_p = pj;
-      }
-    }
-    if (t < T && e < k) {
-      const float w = p.normalize != 0 ? my_p / wsum : my_p;
-      ids[t * k + e] = my_id;
-      atomicAdd(&cnt[my_id], 1);  // counts only; order-independent
+    int64_t t;
+    int id;
+    float w;
+    if (route_group<LT>(xl, t0, T, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
+      const int e = lane % (kWave / tpw);
+      ids[t * k + e] = id;
+      atomicAdd(&cnt[id], 1);  // counts only; order-independent
       if (publish) {
-        p.topk_ids[t * k + e] = my_id;
+        p.topk_ids[t * k + e] = id;
         p.topk_w[t * k + e] = w;
       }
     }

@@ -121,14 +121,29 @@ __global__ void __launch_bounds__(1024) route_dispatch_small_kernel(RouteArgs a)
   const int nwaves = blockDim.x / kWave;
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  for (int64_t t = wave; t < T; t += nwaves) {
-    int id;
-    float w;
-    route_token<LT, VPL>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
-    if (lane < k) {
-      p.topk_ids[t * k + lane] = id;
-      p.topk_w[t * k + lane] = w;
-      atomicAdd(&cnt[id], 1);  // counts only; order-independent
+  if constexpr (VPL == 1) {  // E <= 64: several tokens per wave (route_group)
+    const int tpw = route_group_tokens(E);
+    for (int64_t t0 = static_cast<int64_t>(wave) * tpw; t0 < T; t0 += static_cast<int64_t>(nwaves) * tpw) {
+      int64_t t;
+      int id;
+      float w;
+      if (route_group<LT>(p.logits, t0, T, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
+        const int e = lane % (kWave / tpw);
+        p.topk_ids[t * k + e] = id;
+        p.topk_w[t * k + e] = w;
+        atomicAdd(&cnt[id], 1);  // counts only; order-independent
+      }
+    }
+  } else {
+    for (int64_t t = wave; t < T; t += nwaves) {
+      int id;
+      float w;
+      route_token<LT, VPL>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
+      if (lane < k) {
+        p.topk_ids[t * k + lane] = id;
+        p.topk_w[t * k + lane] = w;
+        atomicAdd(&cnt[id], 1);  // counts only; order-independent
+      }
     }
   }
   __syncthreads();
@@ -152,14 +167,29 @@ __global__ void __launch_bounds__(1024) route_hist_kernel(RouteArgs a, int32_t* 
   __syncthreads();
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRouteTokensPerBlock;
   const int64_t t1 = t0 + kRouteTokensPerBlock < T ? t0 + kRouteTokensPerBlock : T;
-  for (int64_t t = t0 + wave; t < t1; t += nwaves) {
-    int id;
-    float w;
-    route_token<LT, VPL>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
-    if (lane < k) {
-      p.topk_ids[t * k + lane] = id;
-      p.topk_w[t * k + lane] = w;
-      atomicAdd(&cnt[id], 1);
+  if constexpr (VPL == 1) {  // E <= 64: several tokens per wave (route_group)
+    const int tpw = route_group_tokens(E);
+    for (int64_t tb = t0 + static_cast<int64_t>(wave) * tpw; tb < t1; tb += static_cast<int64_t>(nwaves) * tpw) {
+      int64_t t;
+      int id;
+      float w;
+      if (route_group<LT>(p.logits, tb, t1, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
+        const int e = lane % (kWave / tpw);
+        p.topk_ids[t * k + e] = id;
+        p.topk_w[t * k + e] = w;
+        atomicAdd(&cnt[id], 1);
+      }
+    }
+  } else {
+    for (int64_t t = t0 + wave; t < t1; t += nwaves) {
+      int id;
+      float w;
+      route_token<LT, VPL>(p.logits, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
+      if (lane < k) {
+        p.topk_ids[t * k + lane] = id;
+        p.topk_w[t * k + lane] = w;
+        atomicAdd(&cnt[id], 1);
+      }
     }
   }
   __syncthreads();
