@@ -197,6 +197,28 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
 }
 
+// One fp16 plane (fp16 prefill without a K split), H a multiple of 8: one
+// thread per (token, 8 features), 16-byte loads and stores, the same sums in
+// the same order as finalize_kernel.
+__global__ void __launch_bounds__(256) finalize_half8_kernel(ExpertArgs a) {
+  const int64_t t = blockIdx.x;
+  const int64_t h0 = (static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x) * 8;
+  if (h0 >= a.H) return;
+  const _Float16* y2h = reinterpret_cast<const _Float16*>(a.y2);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t j = 0; j < a.k; ++j) {
+    const int64_t f = t * a.k + j;
+    const float w = a.topk_w[f];
+    const half8_t v = *reinterpret_cast<const half8_t*>(y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H + h0);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] += w * static_cast<float>(v[c]);
+  }
+  half8_t o;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = static_cast<_Float16>(acc[c]);
+  *reinterpret_cast<half8_t*>(static_cast<_Float16*>(a.out) + t * a.H + h0) = o;
+}
+
 }  // namespace
 
 hipError_t launch_fc1_simt(const ExpertArgs& a, hipStream_t stream) {
@@ -217,6 +239,11 @@ hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream) {
 
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream) {
   if (a.T == 0) return hipSuccess;
+  if (a.y2_half && a.act_type == MOE_ELEM_FLOAT16 && a.H % 8 == 0) {
+    const dim3 grid8(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + 2047) / 2048));
+    hipLaunchKernelGGL(finalize_half8_kernel, grid8, dim3(256), 0, stream, a);
+    return hipGetLastError();
+  }
   dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + 1023) / 1024));
   switch (a.act_type) {
     case MOE_ELEM_FLOAT: hipLaunchKernelGGL(finalize_kernel<F32>, grid, dim3(256), 0, stream, a); break;
