@@ -83,7 +83,7 @@ struct StreamStage {
 // Largest T * k and expert count for which the decode fc1 kernel routes in
 // its prologue.
 constexpr int kFusedRouteRows = 1024;
-constexpr int kFusedRouteExperts = 64;
+constexpr int kFusedRouteExperts = 128;
 
 template <int WF, bool GATED>
 struct SGeo {

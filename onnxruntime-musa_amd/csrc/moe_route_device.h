@@ -116,8 +116,8 @@ __device__ __forceinline__ int id_bits(int E) {
 // expert): the values the router/dispatch kernels produce.  With publish,
 // the workgroup also writes topk_ids, topk_w, offsets, perm and inv_perm of
 // p to global memory.  scratch: route_block_scratch_bytes() of LDS.  Needs
-// E <= 64 (one expert per lane in the scan); every thread of the workgroup
-// calls it.
+// E <= 128 (at most two experts per lane in the scan); every thread of the
+// workgroup calls it.
 //
 // The logits are first copied to LDS with one load per element: when every
 // workgroup of a grid routes the same batch, a load per token and wave would
@@ -199,35 +199,60 @@ __device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* 
   for (int i = tid; i < T * E; i += blockDim.x) xl[i] = xg[i];
   for (int i = tid; i < E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
-  // tokens in lane groups (route_group)
-  const int tpw = route_group_tokens(E);
-  for (int t0 = wave * tpw; t0 < T; t0 += nwaves * tpw) {
-    int64_t t;
-    int id;
-    float w;
-    if (route_group<LT>(xl, t0, T, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
-      const int e = lane % (kWave / tpw);
-      ids[t * k + e] = id;
-      atomicAdd(&cnt[id], 1);  // counts only; order-independent
-      if (publish) {
-        p.topk_ids[t * k + e] = id;
-        p.topk_w[t * k + e] = w;
+  if (E <= kWave) {
+    // tokens in lane groups (route_group)
+    const int tpw = route_group_tokens(E);
+    for (int t0 = wave * tpw; t0 < T; t0 += nwaves * tpw) {
+      int64_t t;
+      int id;
+      float w;
+      if (route_group<LT>(xl, t0, T, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
+        const int e = lane % (kWave / tpw);
+        ids[t * k + e] = id;
+        atomicAdd(&cnt[id], 1);  // counts only; order-independent
+        if (publish) {
+          p.topk_ids[t * k + e] = id;
+          p.topk_w[t * k + e] = w;
+        }
+      }
+    }
+  } else {
+    // 65..128 experts: one wavefront per token, two experts per lane
+    for (int t = wave; t < T; t += nwaves) {
+      int id;
+      float w;
+      route_token<LT, 2>(xl, t, E, k, p.normalize != 0, p.sigmoid != 0, lane, &id, &w);
+      if (lane < k) {
+        ids[t * k + lane] = id;
+        atomicAdd(&cnt[id], 1);
+        if (publish) {
+          p.topk_ids[t * k + lane] = id;
+          p.topk_w[t * k + lane] = w;
+        }
       }
     }
   }
   __syncthreads();
   if (wave == 0) {
-    const int c = lane < E ? cnt[lane] : 0;
-    int inc = c;
+    // experts 2 lane and 2 lane + 1 (E <= 128)
+    const int e0 = 2 * lane, e1 = 2 * lane + 1;
+    const int c0 = e0 < E ? cnt[e0] : 0, c1 = e1 < E ? cnt[e1] : 0;
+    int inc = c0 + c1;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       const int v = __shfl_up(inc, o, kWave);
       if (lane >= o) inc += v;
     }
-    if (lane < E) {
-      offs[lane] = inc - c;
-      base[lane] = inc - c;
-      if (publish) p.offsets[lane] = inc - c;
+    const int ex = inc - c0 - c1;
+    if (e0 < E) {
+      offs[e0] = ex;
+      base[e0] = ex;
+      if (publish) p.offsets[e0] = ex;
+    }
+    if (e1 < E) {
+      offs[e1] = ex + c0;
+      base[e1] = ex + c0;
+      if (publish) p.offsets[e1] = ex + c0;
     }
     if (lane == kWave - 1) {
       offs[E] = inc;

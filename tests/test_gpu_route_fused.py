@@ -1,6 +1,6 @@
 """Routing inside the decode fc1 kernel.
 
-Small decode batches (T * k <= 1024, E <= 64) are routed and dispatched by
+Small decode batches (T * k <= 1024, E <= 128) are routed and dispatched by
 every workgroup of the fc1 kernel in its prologue, and workgroup 0 writes the
 results out for fc2 and finalize.  These cases check those results (ids,
 offsets, permutation bit-exact; weights to fp32 rounding) and the layer
@@ -28,8 +28,10 @@ SMALL5 = dict(hidden=256, inter=192)
     (8, 2, 1), (8, 8, 64),       # every expert taken by every token
     (64, 16, 64),                # T k = 1024: the largest batch routed in fc1
     (64, 17, 61),                # T k = 1037: router kernels
-    (65, 2, 16),                 # E = 65: router kernels
-    (128, 8, 16),                # router kernels
+    (65, 2, 16),                 # two experts per lane from here on
+    (128, 8, 16), (128, 8, 64),  # E = 128: the most experts routed in fc1
+    (128, 64, 16),               # k = 64 (the op's limit), T k = 1024
+    (129, 4, 16),                # E = 129: router kernels
     (33, 5, 7),
 ])
 def test_decode_routing_limits(cuda, E, k, T):
