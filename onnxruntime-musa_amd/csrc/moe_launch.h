@@ -27,8 +27,10 @@ constexpr int64_t kMaxExperts = 512;
 constexpr int64_t kMaxTopK = 64;
 // Token count up to which routing + dispatch runs as one single-workgroup kernel.
 constexpr int64_t kSmallRouteTokens = 256;
-// Tokens routed per workgroup in the multi-workgroup router.
-constexpr int kRouteTokensPerBlock = 64;
+// Tokens routed per workgroup in the multi-workgroup router: one token per
+// wave of its 16 when experts take two per lane (E > 64), and enough
+// workgroups to cover the CUs (8192 tokens: 512 workgroups).
+constexpr int kRouteTokensPerBlock = 16;
 
 struct RouteArgs {
   moe_route_params p;
