@@ -5,11 +5,12 @@
 // (musa/ep/src/kernels/math/softmax_impl.mu:49-84).
 //
 // The input is viewed as [outer, dim, inner].  With inner == 1 one wavefront
-// takes a row.  For long rows each lane keeps a running maximum and a sum of
-// exponentials rescaled whenever its maximum rises, the lanes' pairs merge
-// in a butterfly, and a second pass writes -- two reads of the row instead of
-// three (max, sum, write), which short rows keep.
-// Otherwise one thread takes an (outer, inner) position and walks dim, so
+// takes a row.  Rows up to 4096 long stay in registers between the max, sum
+// and write steps, so each is read once.  For longer rows each lane keeps a
+// running maximum and a sum of exponentials rescaled whenever its maximum
+// rises, the lanes' pairs merge in a butterfly, and a second pass writes --
+// two reads of the row instead of three (max, sum, write).
+// Otherwise (inner > 1) one thread takes an (outer, inner) position and walks dim, so
 // that neighbouring threads read neighbouring inner elements.
 #include <stdint.h>
 
@@ -60,12 +61,51 @@ __device__ __forceinline__ A sm_wave_sum(A v) {
   return v;
 }
 
-// Rows at least this long take the online max-and-sum pass (16 elements per
-// lane or more); shorter ones spend less on a max pass, a sum pass and plain
-// butterflies than on the exponentials of the online merge.
-constexpr int64_t kOnlineDim = 1024;
+// Rows longer than 64 * kCachedMaxNv take softmax_rows_kernel (128 values
+// per lane would pass the 256 VGPRs of a wave and spill).
+constexpr int kCachedMaxNv = 64;
 
-// inner == 1: one wavefront per row
+// inner == 1 and dim <= 64 NV: one wavefront per row, the row held in
+// registers (NV elements per lane, d = lane + 64 i), so it is read once: the
+// exponentials computed for the sum are the ones written.
+template <typename T, typename A, int NV>
+__global__ void __launch_bounds__(256) softmax_rows_cached_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                                  int64_t rows, int64_t dim) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wpb = blockDim.x / kWave;
+  const int d = static_cast<int>(dim);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * wpb) {
+    const T* x = in + r * dim;
+    A v[NV];
+    A m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + kWave * i;
+      v[i] = c < d ? sm_load<T, A>(x, c) : static_cast<A>(-INFINITY);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) m = v[i] > m ? v[i] : m;
+    m = sm_wave_max(m);
+    A s = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (lane + kWave * i < d) {
+        v[i] = sm_exp(v[i] - m);
+        s += v[i];
+      }
+    }
+    const A inv = static_cast<A>(1) / sm_wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + kWave * i;
+      if (c < d) sm_store<T, A>(out + r * dim, c, v[i] * inv);
+    }
+  }
+}
+
+// inner == 1, longer rows: one wavefront per row, the
+// online max-and-sum pass then the write pass
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                            int64_t rows, int64_t dim) {
@@ -75,33 +115,23 @@ __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__
        r += static_cast<int64_t>(gridDim.x) * wpb) {
     const T* x = in + r * dim;
     A m = -INFINITY, s = 0;
-    if (dim >= kOnlineDim) {
-      for (int64_t d = lane; d < dim; d += kWave) {
-        const A v = sm_load<T, A>(x, d);
-        if (v > m) {
-          s = s * sm_exp(m - v) + static_cast<A>(1);  // exp(-inf) = 0 on a lane's first element
-          m = v;
-        } else if (m != -INFINITY) {  // -inf elements before any finite one add nothing
-          s += sm_exp(v - m);
-        }
+    for (int64_t d = lane; d < dim; d += kWave) {
+      const A v = sm_load<T, A>(x, d);
+      if (v > m) {
+        s = s * sm_exp(m - v) + static_cast<A>(1);  // exp(-inf) = 0 on a lane's first element
+        m = v;
+      } else if (m != -INFINITY) {  // -inf elements before any finite one add nothing
+        s += sm_exp(v - m);
       }
+    }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const A om = __shfl_xor(m, o, kWave), os = __shfl_xor(s, o, kWave);
-        const A nm = om > m ? om : m;
-        // a side with nothing summed yet (s = 0, m = -inf) adds nothing
-        s = (m == nm ? s : (s == 0 ? static_cast<A>(0) : s * sm_exp(m - nm))) +
-            (om == nm ? os : (os == 0 ? static_cast<A>(0) : os * sm_exp(om - nm)));
-        m = nm;
-      }
-    } else {
-      for (int64_t d = lane; d < dim; d += kWave) {
-        const A v = sm_load<T, A>(x, d);
-        m = v > m ? v : m;
-      }
-      m = sm_wave_max(m);
-      for (int64_t d = lane; d < dim; d += kWave) s += sm_exp(sm_load<T, A>(x, d) - m);
-      s = sm_wave_sum(s);
+    for (int o = 32; o > 0; o >>= 1) {
+      const A om = __shfl_xor(m, o, kWave), os = __shfl_xor(s, o, kWave);
+      const A nm = om > m ? om : m;
+      // a side with nothing summed yet (s = 0, m = -inf) adds nothing
+      s = (m == nm ? s : (s == 0 ? static_cast<A>(0) : s * sm_exp(m - nm))) +
+          (om == nm ? os : (os == 0 ? static_cast<A>(0) : os * sm_exp(om - nm)));
+      m = nm;
     }
     const A inv = static_cast<A>(1) / s;
     for (int64_t d = lane; d < dim; d += kWave) sm_store<T, A>(out + r * dim, d, sm_exp(sm_load<T, A>(x, d) - m) * inv);
@@ -136,8 +166,16 @@ hipError_t launch_typed(const void* in, void* out, int64_t outer, int64_t dim, i
   T* y = static_cast<T*>(out);
   if (inner == 1) {
     const int64_t blocks = (outer + 3) / 4;  // 4 waves per block
-    hipLaunchKernelGGL((softmax_rows_kernel<T, A>), dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),
-                       dim3(256), 0, stream, x, y, outer, dim);
+    const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+    if (dim <= kWave * 4)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 4>), grid, dim3(256), 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * 16)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 16>), grid, dim3(256), 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * kCachedMaxNv)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, kCachedMaxNv>), grid, dim3(256), 0, stream, x, y, outer,
+                         dim);
+    else
+      hipLaunchKernelGGL((softmax_rows_kernel<T, A>), grid, dim3(256), 0, stream, x, y, outer, dim);
   } else {
     const int64_t n = outer * inner, blocks = (n + 255) / 256;
     hipLaunchKernelGGL((softmax_strided_kernel<T, A>), dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),

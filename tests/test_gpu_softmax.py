@@ -40,7 +40,8 @@ def test_reference_cases(cuda):
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 @pytest.mark.parametrize("shape,axis", [((3, 1000), -1), ((7, 4097), 1), ((5, 6, 33), 1), ((2, 300, 4), 0),
-                                        ((8192, 128), -1), ((1, 1), 0)])
+                                        ((8192, 128), -1), ((1, 1), 0),
+                                        ((3, 256), -1), ((4, 257), -1), ((9, 2500), -1), ((5, 4096), -1)])
 def test_shapes(cuda, dt, shape, axis):
     run(cuda, 3.0 * np.random.default_rng(sum(shape)).standard_normal(shape), axis, dt)
 
@@ -50,7 +51,7 @@ def test_large_values_are_shift_invariant(cuda):
     run(cuda, x, -1)
 
 
-@pytest.mark.parametrize("dim", [200, 3000])
+@pytest.mark.parametrize("dim", [200, 3000, 5000])
 def test_masked_rows(cuda, dim):
     # -inf (masked) entries, some rows led by a masked prefix, one row all but one masked
     x = np.random.default_rng(dim).standard_normal((6, dim)).astype(np.float32)
