@@ -5,13 +5,14 @@
 // (musa/ep/src/kernels/math/softmax_impl.mu:49-84).
 //
 // The input is viewed as [outer, dim, inner].  With inner == 1 one wavefront
-// takes a row.  Rows up to 4096 long stay in registers between the max, sum
-// and write steps, so each is read once.  For longer rows each lane keeps a
-// running maximum and a sum of exponentials rescaled whenever its maximum
-// rises, the lanes' pairs merge in a butterfly, and a second pass writes --
-// two reads of the row instead of three (max, sum, write).
-// Otherwise (inner > 1) one thread takes an (outer, inner) position and walks dim, so
-// that neighbouring threads read neighbouring inner elements.
+// takes a row, or 2 or 4 wavefronts of a workgroup share it.  Rows up to
+// 16384 long stay in registers between the max, sum and write steps, so each
+// is read once.  A longer row takes a workgroup: each thread keeps a running
+// maximum and a sum of exponentials rescaled whenever its maximum rises, the
+// threads' pairs merge, and a second pass writes -- two reads of the row
+// instead of three (max, sum, write).  Otherwise (inner > 1) one thread takes
+// an (outer, inner) position and walks dim, so that neighbouring threads read
+// neighbouring inner elements.
 #include <stdint.h>
 
 #include "moe_device.h"
@@ -61,80 +62,135 @@ __device__ __forceinline__ A sm_wave_sum(A v) {
   return v;
 }
 
-// Rows longer than 64 * kCachedMaxNv take softmax_rows_kernel (128 values
-// per lane would pass the 256 VGPRs of a wave and spill).
+// Values per lane of the register-held rows: the smallest of 4, 16 and 32
+// that holds a row over 1, 2 or 4 waves (fewer registers, more waves per
+// SIMD), then 64 for rows of 8193..16384; 128 would pass the 256 VGPRs of a
+// wave and spill.
 constexpr int kCachedMaxNv = 64;
+// Most wavefronts sharing one register-held row (rows up to 64 * 64 * 4 =
+// 16384); longer rows take softmax_rows_kernel.
+constexpr int kCachedMaxWaves = 4;
 
-// inner == 1 and dim <= 64 NV: one wavefront per row, the row held in
-// registers (NV elements per lane, d = lane + 64 i), so it is read once: the
-// exponentials computed for the sum are the ones written.
-template <typename T, typename A, int NV>
+// inner == 1 and dim <= 64 NV WPR: WPR wavefronts of a workgroup take one row,
+// held in registers (NV elements per lane, d = lane + 64 (w + WPR i) for the
+// row's wave w), so it is read once: the exponentials computed for the sum
+// are the ones written.  Waves of one row combine their maxima and sums in
+// LDS.
+template <typename T, typename A, int NV, int WPR>
 __global__ void __launch_bounds__(256) softmax_rows_cached_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                                   int64_t rows, int64_t dim) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wpb = blockDim.x / kWave;
+  __shared__ A part[2][256 / kWave];  // per-wave maximum, sum
+  const int lane = threadIdx.x & 63, wave = threadIdx.x / kWave;
+  const int w = wave % WPR, first = wave - w;
+  const int64_t rpb = blockDim.x / kWave / WPR;
   const int d = static_cast<int>(dim);
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; r < rows;
-       r += static_cast<int64_t>(gridDim.x) * wpb) {
-    const T* x = in + r * dim;
+  // every wave of a workgroup runs the same iterations (uniform barriers)
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * rpb; r0 < rows; r0 += static_cast<int64_t>(gridDim.x) * rpb) {
+    const int64_t r = r0 + wave / WPR;
+    const bool live = r < rows;
+    const T* x = in + (live ? r : 0) * dim;
     A v[NV];
     A m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int c = lane + kWave * i;
-      v[i] = c < d ? sm_load<T, A>(x, c) : static_cast<A>(-INFINITY);
+      const int c = lane + kWave * (w + WPR * i);
+      v[i] = live && c < d ? sm_load<T, A>(x, c) : static_cast<A>(-INFINITY);
     }
 #pragma unroll
     for (int i = 0; i < NV; ++i) m = v[i] > m ? v[i] : m;
     m = sm_wave_max(m);
+    if constexpr (WPR > 1) {
+      if (lane == 0) part[0][wave] = m;
+      __syncthreads();
+#pragma unroll
+      for (int o = 0; o < WPR; ++o) m = part[0][first + o] > m ? part[0][first + o] : m;
+    }
     A s = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      if (lane + kWave * i < d) {
+      if (lane + kWave * (w + WPR * i) < d) {
         v[i] = sm_exp(v[i] - m);
         s += v[i];
       }
     }
-    const A inv = static_cast<A>(1) / sm_wave_sum(s);
+    s = sm_wave_sum(s);
+    if constexpr (WPR > 1) {
+      if (lane == 0) part[1][wave] = s;
+      __syncthreads();  // also orders this row's reads of part[0] before the next row's writes
+      s = 0;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int c = lane + kWave * i;
-      if (c < d) sm_store<T, A>(out + r * dim, c, v[i] * inv);
+      for (int o = 0; o < WPR; ++o) s += part[1][first + o];
+    }
+    const A inv = static_cast<A>(1) / s;
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int c = lane + kWave * (w + WPR * i);
+        if (c < d) sm_store<T, A>(out + r * dim, c, v[i] * inv);
+      }
     }
   }
 }
 
-// inner == 1, longer rows: one wavefront per row, the
-// online max-and-sum pass then the write pass
+// Running (maximum, sum of exponentials) of one more value; exp(-inf) = 0 on
+// a thread's first element, and -inf elements before any finite one add
+// nothing.
+template <typename A>
+__device__ __forceinline__ void sm_online(A& m, A& s, A v) {
+  if (v > m) {
+    s = s * sm_exp(m - v) + static_cast<A>(1);
+    m = v;
+  } else if (m != -INFINITY) {
+    s += sm_exp(v - m);
+  }
+}
+
+// Merges the pair (om, os) into (m, s); a side with nothing summed yet
+// (s = 0, m = -inf) adds nothing.
+template <typename A>
+__device__ __forceinline__ void sm_merge(A& m, A& s, A om, A os) {
+  const A nm = om > m ? om : m;
+  s = (m == nm ? s : (s == 0 ? static_cast<A>(0) : s * sm_exp(m - nm))) +
+      (om == nm ? os : (os == 0 ? static_cast<A>(0) : os * sm_exp(om - nm)));
+  m = nm;
+}
+
+// inner == 1, rows longer than the register-held ones: one workgroup per
+// row, the online max-and-sum pass (four loads in flight per thread), the
+// threads' pairs merged in a butterfly and then across the 4 waves in LDS,
+// then the write pass.
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                            int64_t rows, int64_t dim) {
-  const int lane = threadIdx.x & 63;
-  const int64_t wpb = blockDim.x / kWave;
-  for (int64_t r = static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave; r < rows;
-       r += static_cast<int64_t>(gridDim.x) * wpb) {
+  __shared__ A part[2][256 / kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid / kWave;
+  const int nt = blockDim.x, nw = blockDim.x / kWave;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const T* x = in + r * dim;
     A m = -INFINITY, s = 0;
-    for (int64_t d = lane; d < dim; d += kWave) {
-      const A v = sm_load<T, A>(x, d);
-      if (v > m) {
-        s = s * sm_exp(m - v) + static_cast<A>(1);  // exp(-inf) = 0 on a lane's first element
-        m = v;
-      } else if (m != -INFINITY) {  // -inf elements before any finite one add nothing
-        s += sm_exp(v - m);
-      }
-    }
+    int64_t d = tid;
+    for (; d + 3 * nt < dim; d += 4 * nt) {
+      A v[4];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const A om = __shfl_xor(m, o, kWave), os = __shfl_xor(s, o, kWave);
-      const A nm = om > m ? om : m;
-      // a side with nothing summed yet (s = 0, m = -inf) adds nothing
-      s = (m == nm ? s : (s == 0 ? static_cast<A>(0) : s * sm_exp(m - nm))) +
-          (om == nm ? os : (os == 0 ? static_cast<A>(0) : os * sm_exp(om - nm)));
-      m = nm;
+      for (int u = 0; u < 4; ++u) v[u] = sm_load<T, A>(x, d + u * nt);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) sm_online(m, s, v[u]);
     }
+    for (; d < dim; d += nt) sm_online(m, s, sm_load<T, A>(x, d));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sm_merge(m, s, __shfl_xor(m, o, kWave), __shfl_xor(s, o, kWave));
+    if (lane == 0) {
+      part[0][wave] = m;
+      part[1][wave] = s;
+    }
+    __syncthreads();
+    m = part[0][0];
+    s = part[1][0];
+    for (int w = 1; w < nw; ++w) sm_merge(m, s, part[0][w], part[1][w]);
+    __syncthreads();  // every wave has read part before the next row writes it
     const A inv = static_cast<A>(1) / s;
-    for (int64_t d = lane; d < dim; d += kWave) sm_store<T, A>(out + r * dim, d, sm_exp(sm_load<T, A>(x, d) - m) * inv);
+#pragma unroll 4
+    for (int64_t e = tid; e < dim; e += nt) sm_store<T, A>(out + r * dim, e, sm_exp(sm_load<T, A>(x, e) - m) * inv);
   }
 }
 
@@ -165,17 +221,27 @@ hipError_t launch_typed(const void* in, void* out, int64_t outer, int64_t dim, i
   const T* x = static_cast<const T*>(in);
   T* y = static_cast<T*>(out);
   if (inner == 1) {
-    const int64_t blocks = (outer + 3) / 4;  // 4 waves per block
-    const dim3 grid(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+    const dim3 block(256);
+    // rows per workgroup: 4 / (waves per row)
+    auto grid = [outer](int64_t rpb) {
+      const int64_t blocks = (outer + rpb - 1) / rpb;
+      return dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536));
+    };
     if (dim <= kWave * 4)
-      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 4>), grid, dim3(256), 0, stream, x, y, outer, dim);
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 4, 1>), grid(4), block, 0, stream, x, y, outer, dim);
     else if (dim <= kWave * 16)
-      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 16>), grid, dim3(256), 0, stream, x, y, outer, dim);
-    else if (dim <= kWave * kCachedMaxNv)
-      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, kCachedMaxNv>), grid, dim3(256), 0, stream, x, y, outer,
-                         dim);
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 16, 1>), grid(4), block, 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * 32)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 32, 1>), grid(4), block, 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * 32 * 2)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 32, 2>), grid(2), block, 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * 32 * 4)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 32, 4>), grid(1), block, 0, stream, x, y, outer, dim);
+    else if (dim <= kWave * kCachedMaxNv * kCachedMaxWaves)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, kCachedMaxNv, kCachedMaxWaves>), grid(1), block, 0, stream,
+                         x, y, outer, dim);
     else
-      hipLaunchKernelGGL((softmax_rows_kernel<T, A>), grid, dim3(256), 0, stream, x, y, outer, dim);
+      hipLaunchKernelGGL((softmax_rows_kernel<T, A>), grid(1), block, 0, stream, x, y, outer, dim);
   } else {
     const int64_t n = outer * inner, blocks = (n + 255) / 256;
     hipLaunchKernelGGL((softmax_strided_kernel<T, A>), dim3(static_cast<unsigned>(blocks < 65536 ? blocks : 65536)),

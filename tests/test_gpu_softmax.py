@@ -41,7 +41,9 @@ def test_reference_cases(cuda):
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 @pytest.mark.parametrize("shape,axis", [((3, 1000), -1), ((7, 4097), 1), ((5, 6, 33), 1), ((2, 300, 4), 0),
                                         ((8192, 128), -1), ((1, 1), 0),
-                                        ((3, 256), -1), ((4, 257), -1), ((9, 2500), -1), ((5, 4096), -1)])
+                                        ((3, 256), -1), ((4, 257), -1), ((3, 1500), -1), ((4, 2048), -1), ((9, 2500), -1), ((5, 4096), -1),
+                                        ((7, 6000), -1), ((3, 8192), -1), ((5, 8193), -1), ((2, 16384), -1),
+                                        ((3, 16385), -1), ((2, 33000), -1)])
 def test_shapes(cuda, dt, shape, axis):
     run(cuda, 3.0 * np.random.default_rng(sum(shape)).standard_normal(shape), axis, dt)
 
@@ -51,7 +53,7 @@ def test_large_values_are_shift_invariant(cuda):
     run(cuda, x, -1)
 
 
-@pytest.mark.parametrize("dim", [200, 3000, 5000])
+@pytest.mark.parametrize("dim", [200, 3000, 5000, 12000, 20000])
 def test_masked_rows(cuda, dim):
     # -inf (masked) entries, some rows led by a masked prefix, one row all but one masked
     x = np.random.default_rng(dim).standard_normal((6, dim)).astype(np.float32)
