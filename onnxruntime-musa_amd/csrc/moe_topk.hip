@@ -4,14 +4,15 @@
 //
 // Axes up to 512 with k <= 32: lane groups of a wavefront take a slice each,
 // k rounds of a group arg-max over keys held in registers
-// (topk_wave_kernel).  Otherwise one
-// workgroup per (row, inner) slice of the input viewed as [rows, dim,
-// inner].  The slice's dim elements become order-preserving integer keys in
-// LDS (floats: sign-magnitude bits flipped to two's-complement order, -0.0
-// folded onto +0.0 so that it ties with +0.0 as a value comparison does;
-// integers: sign bit flipped; smallest-first negates the key), padded to a
-// power of two with keys that sort last, and a bitonic network sorts (key
-// desc, index asc).  The first k entries are written out; values are read
+// (topk_wave_kernel).  Axes up to 8192 with k <= 64: the same rounds over a
+// workgroup (topk_block_kernel).  Otherwise one workgroup per (row, inner)
+// slice of the input viewed as [rows, dim, inner] sorts it: the slice's dim
+// elements become order-preserving integer keys in LDS (floats:
+// sign-magnitude bits flipped to two's-complement order, -0.0 folded onto
+// +0.0 so that it ties with +0.0 as a value comparison does; integers: sign
+// bit flipped; smallest-first negates the key; the register kernels use the
+// same keys), padded to a power of two with keys that sort last, and a
+// bitonic network sorts (key desc, index asc).  The first k entries are written out; values are read
 // back from the input at their index, so they keep their exact bits.
 //
 // NaN keys sort as the largest values (above +inf) for largest = 1 and the
@@ -110,7 +111,7 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
 // slices per wavefront), every lane holding kWaveVpl (key, index) entries
 // in registers; k rounds of a group arg-max (log2 G butterfly steps) under
 // the same order (key desc, index asc) pick the outputs in sorted order --
-// no LDS, no barriers.
+// no LDS, no barriers.  The outputs are written after the last round.
 constexpr int kWaveVpl = 8;
 constexpr int kWaveMaxK = 32;
 
@@ -137,6 +138,10 @@ __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in
       const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
       key[v] = p.largest ? kv : ~kv;
     }
+    constexpr int kWins = (kWaveMaxK + G - 1) / G;  // rounds kept per lane
+    uint32_t win[kWins];
+#pragma unroll
+    for (int q = 0; q < kWins; ++q) win[q] = 0;
     for (int j = 0; j < k; ++j) {
       uint64_t bk = 0;
       uint32_t bi = 0xFFFFFFFFu;
@@ -159,16 +164,114 @@ __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in
           bi = oi;
         }
       }
-      // the owner of the winner retires it and writes the output
+      // the owner of the winner retires it; lane j % G keeps round j's winner
       if (valid && static_cast<int>(bi % G) == sub) {
 #pragma unroll
         for (int v = 0; v < kWaveVpl; ++v)
           if (v == static_cast<int>(bi / G)) live[v] = false;
-        const int64_t o = (row * p.k + j) * p.inner + in0;
-        values[o] = src[static_cast<int64_t>(bi) * p.inner];
-        indices[o] = static_cast<int64_t>(bi);
+      }
+#pragma unroll
+      for (int q = 0; q < kWins; ++q)
+        if (q * G + sub == j) win[q] = bi;
+    }
+    // the k value reads go out together instead of one per round
+    if (valid) {
+#pragma unroll
+      for (int q = 0; q < kWins; ++q) {
+        const int j = q * G + sub;
+        if (j < k) {
+          const int64_t o = (row * p.k + j) * p.inner + in0;
+          values[o] = src[static_cast<int64_t>(win[q]) * p.inner];
+          indices[o] = static_cast<int64_t>(win[q]);
+        }
       }
     }
+  }
+}
+
+// Axes up to 8192 with k <= 64: one workgroup of 256 threads per slice, each
+// thread holding VPL (key, index) entries (i = tid + 256 v) in registers; k
+// rounds of a workgroup arg-max: a wave butterfly, then the 4 waves' winners
+// compared in LDS (two buffers by round parity, so one barrier a round).
+// Each element is read once; the k rounds replace a full sort of the slice.
+constexpr int kBlockMaxK = 64;
+
+template <typename T, int VPL>
+__global__ void __launch_bounds__(256) topk_block_kernel(const T* __restrict__ in, T* __restrict__ values,
+                                                         int64_t* __restrict__ indices, TopKArgs p) {
+  __shared__ uint64_t wkey[2][256 / kWave];
+  __shared__ uint32_t widx[2][256 / kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid / kWave;
+  const int nt = blockDim.x, nw = blockDim.x / kWave;
+  const int64_t slices = p.rows * p.inner;
+  const int dim = static_cast<int>(p.dim), k = static_cast<int>(p.k);
+  for (int64_t sl = blockIdx.x; sl < slices; sl += gridDim.x) {  // uniform per workgroup
+    const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
+    const T* src = in + row * p.dim * p.inner + in0;
+    uint64_t key[VPL];
+    bool live[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int i = tid + nt * v;
+      live[v] = i < dim;
+      const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
+      key[v] = p.largest ? kv : ~kv;
+    }
+    uint32_t mine = 0;  // the winner of round tid
+    for (int j = 0; j < k; ++j) {
+      uint64_t bk = 0;
+      uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const uint32_t i = static_cast<uint32_t>(tid + nt * v);
+        if (live[v] && entry_before(key[v], i, bk, bi)) {
+          bk = key[v];
+          bi = i;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, kWave));
+        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, kWave));
+        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, kWave));
+        const uint64_t ok = (static_cast<uint64_t>(ohi) << 32) | olo;
+        if (entry_before(ok, oi, bk, bi)) {
+          bk = ok;
+          bi = oi;
+        }
+      }
+      const int b = j & 1;
+      if (lane == 0) {
+        wkey[b][wave] = bk;
+        widx[b][wave] = bi;
+      }
+      // buffer b is next written in round j + 2, after every thread has
+      // passed round j + 1's barrier and so finished these reads
+      __syncthreads();
+      bk = wkey[b][0];
+      bi = widx[b][0];
+      for (int w = 1; w < nw; ++w) {
+        if (entry_before(wkey[b][w], widx[b][w], bk, bi)) {
+          bk = wkey[b][w];
+          bi = widx[b][w];
+        }
+      }
+      // j < k <= dim, so the winner is a live entry; its owner retires it
+      if (static_cast<int>(bi % static_cast<uint32_t>(nt)) == tid) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v)
+          if (v == static_cast<int>(bi / static_cast<uint32_t>(nt))) live[v] = false;
+      }
+      if (tid == j) mine = bi;
+    }
+    // thread j writes output j: the k value reads go out together instead of
+    // one per round
+    if (tid < k) {
+      const int64_t o = (row * p.k + tid) * p.inner + in0;
+      values[o] = src[static_cast<int64_t>(mine) * p.inner];
+      indices[o] = static_cast<int64_t>(mine);
+    }
+    __syncthreads();  // the next slice's first rounds reuse both buffers
   }
 }
 
@@ -191,6 +294,18 @@ hipError_t launch_typed(const void* in, void* values, int64_t* indices, const To
       case 32: hipLaunchKernelGGL((topk_wave_kernel<T, 32>), grid, dim3(256), 0, stream, x, v, indices, p); break;
       default: hipLaunchKernelGGL((topk_wave_kernel<T, 64>), grid, dim3(256), 0, stream, x, v, indices, p); break;
     }
+    return hipGetLastError();
+  }
+  if (p.k <= kBlockMaxK && p.dim <= 256 * 32) {
+    const dim3 grid(static_cast<unsigned>(slices < (int64_t{1} << 20) ? slices : (int64_t{1} << 20)));
+    const T* x = static_cast<const T*>(in);
+    T* v = static_cast<T*>(values);
+    if (p.dim <= 256 * 8)
+      hipLaunchKernelGGL((topk_block_kernel<T, 8>), grid, dim3(256), 0, stream, x, v, indices, p);
+    else if (p.dim <= 256 * 16)
+      hipLaunchKernelGGL((topk_block_kernel<T, 16>), grid, dim3(256), 0, stream, x, v, indices, p);
+    else
+      hipLaunchKernelGGL((topk_block_kernel<T, 32>), grid, dim3(256), 0, stream, x, v, indices, p);
     return hipGetLastError();
   }
   int n = 1;

@@ -132,3 +132,32 @@ def test_k_zero_and_errors(cuda):
     with pytest.raises(MoeError) as ei:
         topk(torch.ones((1, 8193), device=cuda), 2)
     assert ei.value.code == 9
+
+
+# Axes of 513..8192 with k <= 64 take the workgroup arg-max kernel (8, 16 or
+# 32 entries per thread); heavy ties and -0.0 next to +0.0 exercise its order.
+@pytest.mark.parametrize("largest", [0, 1])
+@pytest.mark.parametrize("dim,k", [(513, 33), (600, 64), (2048, 64), (2049, 40), (4096, 64), (4097, 1),
+                                   (8192, 64), (8192, 33)])
+def test_workgroup_rounds(cuda, dim, k, largest):
+    x = np.random.default_rng(dim + k).integers(-30, 31, size=(6, dim)).astype(np.float32)
+    x[0, ::7] = -0.0
+    run(cuda, x, k, largest=largest)
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.int32, np.int64])
+def test_workgroup_rounds_dtypes(cuda, dt):
+    x = np.random.default_rng(7).integers(-1000, 1000, size=(3, 3000)).astype(dt)
+    run(cuda, x, 50)
+    run(cuda, x.reshape(3, 1500, 2), 64, axis=1, largest=0)  # strided axis
+
+
+@pytest.mark.parametrize("tdt", [torch.float16, torch.bfloat16])
+def test_workgroup_rounds_half(cuda, tdt):
+    x = np.random.default_rng(11).integers(-200, 200, size=(4, 5000)).astype(np.float32) / 16.0
+    run(cuda, x, 48, torch_dtype=tdt)
+
+
+def test_workgroup_rounds_many_slices(cuda):
+    x = np.random.default_rng(12).standard_normal((700, 1024)).astype(np.float32)
+    run(cuda, x, 64)
