@@ -19,6 +19,8 @@
 // smallest for largest = 0.
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "moe_device.h"
 #include "moe_launch.h"
 
@@ -107,68 +109,121 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
   }
 }
 
+// Candidates of the register kernels.  Elements of 32 bits or less have
+// 32-bit keys (the same order as topk_key): a candidate is then one 64-bit
+// word, key above the complemented index, so that (key desc, index asc) is
+// plain unsigned order and a butterfly step moves two words.  64-bit elements
+// keep a (key, index) pair.  A retired or absent entry is dead(), after every
+// live one.
+__device__ __forceinline__ uint32_t key_f32(float f) {
+  if (f == 0.0f) f = 0.0f;  // -0.0 ties with +0.0
+  const uint32_t b = __builtin_bit_cast(uint32_t, f);
+  return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+
+template <typename T>
+struct Packed {  // T of 32 bits or less
+  using C = uint64_t;
+  static __device__ __forceinline__ uint32_t key(T v);
+  static __device__ __forceinline__ C make(T v, uint32_t i, bool largest) {
+    const uint32_t k = largest ? key(v) : ~key(v);
+    return (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~i);
+  }
+  static __device__ __forceinline__ C dead() { return 0; }
+  static __device__ __forceinline__ bool before(C a, C b) { return a > b; }
+  static __device__ __forceinline__ uint32_t index(C c) { return ~static_cast<uint32_t>(c); }
+  static __device__ __forceinline__ C shfl(C c, int o, int width) {
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(c >> 32), o, width));
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(c & 0xFFFFFFFFu), o, width));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+};
+template <>
+__device__ __forceinline__ uint32_t Packed<float>::key(float v) { return key_f32(v); }
+template <>
+__device__ __forceinline__ uint32_t Packed<_Float16>::key(_Float16 v) { return key_f32(static_cast<float>(v)); }
+template <>
+__device__ __forceinline__ uint32_t Packed<uint16_t>::key(uint16_t v) { return key_f32(bf16_to_f32(v)); }
+template <>
+__device__ __forceinline__ uint32_t Packed<int32_t>::key(int32_t v) { return static_cast<uint32_t>(v) ^ 0x80000000u; }
+
+template <typename T>
+struct Pair {  // 64-bit T
+  struct C {
+    uint64_t k;
+    uint32_t i;
+  };
+  static __device__ __forceinline__ C make(T v, uint32_t i, bool largest) {
+    const uint64_t k = topk_key<T>(v);
+    return C{largest ? k : ~k, i};
+  }
+  static __device__ __forceinline__ C dead() { return C{0, 0xFFFFFFFFu}; }
+  static __device__ __forceinline__ bool before(C a, C b) { return entry_before(a.k, a.i, b.k, b.i); }
+  static __device__ __forceinline__ uint32_t index(C c) { return c.i; }
+  static __device__ __forceinline__ C shfl(C c, int o, int width) {
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(c.k >> 32), o, width));
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(c.k & 0xFFFFFFFFu), o, width));
+    const uint32_t i = static_cast<uint32_t>(__shfl_xor(static_cast<int>(c.i), o, width));
+    return C{(static_cast<uint64_t>(hi) << 32) | lo, i};
+  }
+};
+
+template <typename T>
+using CandOps = std::conditional_t<sizeof(T) <= 4, Packed<T>, Pair<T>>;
+
 // Short axes and small k: lane groups of G lanes take one slice each (64 / G
-// slices per wavefront), every lane holding kWaveVpl (key, index) entries
-// in registers; k rounds of a group arg-max (log2 G butterfly steps) under
-// the same order (key desc, index asc) pick the outputs in sorted order --
-// no LDS, no barriers.  The outputs are written after the last round.
+// slices per wavefront), every lane holding kWaveVpl candidates in
+// registers; k rounds of a group arg-max (log2 G butterfly steps) under the
+// same order (key desc, index asc) pick the outputs in sorted order -- no
+// LDS, no barriers.  The outputs are written after the last round.
 constexpr int kWaveVpl = 8;
 constexpr int kWaveMaxK = 32;
 
 template <typename T, int G>
 __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in, T* __restrict__ values,
                                                         int64_t* __restrict__ indices, TopKArgs p) {
+  using O = CandOps<T>;
+  using C = typename O::C;
   const int lane = threadIdx.x & 63, sub = lane % G;
   constexpr int kPerWave = kWave / G;
   const int64_t wpb = blockDim.x / kWave;
   const int64_t slices = p.rows * p.inner;
   const int dim = static_cast<int>(p.dim), k = static_cast<int>(p.k);
+  const bool largest = p.largest != 0;
   for (int64_t s0 = (static_cast<int64_t>(blockIdx.x) * wpb + threadIdx.x / kWave) * kPerWave; s0 < slices;
        s0 += static_cast<int64_t>(gridDim.x) * wpb * kPerWave) {
     const int64_t sl = s0 + lane / G;
     const bool valid = sl < slices;
     const int64_t row = valid ? sl / p.inner : 0, in0 = valid ? sl - row * p.inner : 0;
     const T* src = in + row * p.dim * p.inner + in0;
-    uint64_t key[kWaveVpl];
-    bool live[kWaveVpl];
+    C e[kWaveVpl];
 #pragma unroll
     for (int v = 0; v < kWaveVpl; ++v) {
       const int i = sub + G * v;
-      live[v] = valid && i < dim;
-      const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
-      key[v] = p.largest ? kv : ~kv;
+      e[v] = valid && i < dim ? O::make(src[static_cast<int64_t>(i) * p.inner], static_cast<uint32_t>(i), largest)
+                              : O::dead();
     }
     constexpr int kWins = (kWaveMaxK + G - 1) / G;  // rounds kept per lane
     uint32_t win[kWins];
 #pragma unroll
     for (int q = 0; q < kWins; ++q) win[q] = 0;
     for (int j = 0; j < k; ++j) {
-      uint64_t bk = 0;
-      uint32_t bi = 0xFFFFFFFFu;
+      C b = e[0];
 #pragma unroll
-      for (int v = 0; v < kWaveVpl; ++v) {
-        const uint32_t i = static_cast<uint32_t>(sub + G * v);
-        if (live[v] && entry_before(key[v], i, bk, bi)) {
-          bk = key[v];
-          bi = i;
-        }
-      }
+      for (int v = 1; v < kWaveVpl; ++v)
+        if (O::before(e[v], b)) b = e[v];
 #pragma unroll
       for (int o = G / 2; o > 0; o >>= 1) {
-        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, G));
-        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, G));
-        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, G));
-        const uint64_t ok = (static_cast<uint64_t>(ohi) << 32) | olo;
-        if (entry_before(ok, oi, bk, bi)) {
-          bk = ok;
-          bi = oi;
-        }
+        const C c = O::shfl(b, o, G);
+        if (O::before(c, b)) b = c;
       }
-      // the owner of the winner retires it; lane j % G keeps round j's winner
+      // j < k <= dim: the winner is live; its owner retires it, and lane
+      // j % G keeps round j's winner
+      const uint32_t bi = O::index(b);
       if (valid && static_cast<int>(bi % G) == sub) {
 #pragma unroll
         for (int v = 0; v < kWaveVpl; ++v)
-          if (v == static_cast<int>(bi / G)) live[v] = false;
+          if (v == static_cast<int>(bi / G)) e[v] = O::dead();
       }
 #pragma unroll
       for (int q = 0; q < kWins; ++q)
@@ -190,77 +245,58 @@ __global__ void __launch_bounds__(256) topk_wave_kernel(const T* __restrict__ in
 }
 
 // Axes up to 8192 with k <= 64: one workgroup of 256 threads per slice, each
-// thread holding VPL (key, index) entries (i = tid + 256 v) in registers; k
-// rounds of a workgroup arg-max: a wave butterfly, then the 4 waves' winners
-// compared in LDS (two buffers by round parity, so one barrier a round).
-// Each element is read once; the k rounds replace a full sort of the slice.
+// thread holding VPL candidates (i = tid + 256 v) in registers; k rounds of
+// a workgroup arg-max: a wave butterfly, then the 4 waves' winners compared
+// in LDS (two buffers by round parity, so one barrier a round).  Each
+// element is read once; the k rounds replace a full sort of the slice.
 constexpr int kBlockMaxK = 64;
 
 template <typename T, int VPL>
 __global__ void __launch_bounds__(256) topk_block_kernel(const T* __restrict__ in, T* __restrict__ values,
                                                          int64_t* __restrict__ indices, TopKArgs p) {
-  __shared__ uint64_t wkey[2][256 / kWave];
-  __shared__ uint32_t widx[2][256 / kWave];
+  using O = CandOps<T>;
+  using C = typename O::C;
+  __shared__ C wbest[2][256 / kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid / kWave;
   const int nt = blockDim.x, nw = blockDim.x / kWave;
   const int64_t slices = p.rows * p.inner;
   const int dim = static_cast<int>(p.dim), k = static_cast<int>(p.k);
+  const bool largest = p.largest != 0;
   for (int64_t sl = blockIdx.x; sl < slices; sl += gridDim.x) {  // uniform per workgroup
     const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
     const T* src = in + row * p.dim * p.inner + in0;
-    uint64_t key[VPL];
-    bool live[VPL];
+    C e[VPL];
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const int i = tid + nt * v;
-      live[v] = i < dim;
-      const uint64_t kv = live[v] ? topk_key<T>(src[static_cast<int64_t>(i) * p.inner]) : 0;
-      key[v] = p.largest ? kv : ~kv;
+      e[v] = i < dim ? O::make(src[static_cast<int64_t>(i) * p.inner], static_cast<uint32_t>(i), largest)
+                     : O::dead();
     }
     uint32_t mine = 0;  // the winner of round tid
     for (int j = 0; j < k; ++j) {
-      uint64_t bk = 0;
-      uint32_t bi = 0xFFFFFFFFu;
+      C b = e[0];
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const uint32_t i = static_cast<uint32_t>(tid + nt * v);
-        if (live[v] && entry_before(key[v], i, bk, bi)) {
-          bk = key[v];
-          bi = i;
-        }
-      }
+      for (int v = 1; v < VPL; ++v)
+        if (O::before(e[v], b)) b = e[v];
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t ohi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk >> 32), o, kWave));
-        const uint32_t olo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bk & 0xFFFFFFFFu), o, kWave));
-        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, kWave));
-        const uint64_t ok = (static_cast<uint64_t>(ohi) << 32) | olo;
-        if (entry_before(ok, oi, bk, bi)) {
-          bk = ok;
-          bi = oi;
-        }
+        const C c = O::shfl(b, o, kWave);
+        if (O::before(c, b)) b = c;
       }
-      const int b = j & 1;
-      if (lane == 0) {
-        wkey[b][wave] = bk;
-        widx[b][wave] = bi;
-      }
-      // buffer b is next written in round j + 2, after every thread has
+      const int buf = j & 1;
+      if (lane == 0) wbest[buf][wave] = b;
+      // buffer buf is next written in round j + 2, after every thread has
       // passed round j + 1's barrier and so finished these reads
       __syncthreads();
-      bk = wkey[b][0];
-      bi = widx[b][0];
-      for (int w = 1; w < nw; ++w) {
-        if (entry_before(wkey[b][w], widx[b][w], bk, bi)) {
-          bk = wkey[b][w];
-          bi = widx[b][w];
-        }
-      }
-      // j < k <= dim, so the winner is a live entry; its owner retires it
+      b = wbest[buf][0];
+      for (int w = 1; w < nw; ++w)
+        if (O::before(wbest[buf][w], b)) b = wbest[buf][w];
+      // j < k <= dim, so the winner is live; its owner retires it
+      const uint32_t bi = O::index(b);
       if (static_cast<int>(bi % static_cast<uint32_t>(nt)) == tid) {
 #pragma unroll
         for (int v = 0; v < VPL; ++v)
-          if (v == static_cast<int>(bi / static_cast<uint32_t>(nt))) live[v] = false;
+          if (v == static_cast<int>(bi / static_cast<uint32_t>(nt))) e[v] = O::dead();
       }
       if (tid == j) mine = bi;
     }
