@@ -161,3 +161,10 @@ def test_workgroup_rounds_half(cuda, tdt):
 def test_workgroup_rounds_many_slices(cuda):
     x = np.random.default_rng(12).standard_normal((700, 1024)).astype(np.float32)
     run(cuda, x, 64)
+
+
+# Many slices through the wave kernel, at lane groups of 4, 16, 4 and 32.
+@pytest.mark.parametrize("rows,dim,k", [(70000, 20, 2), (32768, 100, 5), (20000, 30, 3), (5000, 250, 32)])
+def test_wave_entries_per_lane(cuda, rows, dim, k):
+    x = np.random.default_rng(rows).integers(-40, 41, size=(rows, dim)).astype(np.float32)
+    run(cuda, x, k)
