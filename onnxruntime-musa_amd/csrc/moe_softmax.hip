@@ -11,8 +11,8 @@
 // maximum and a sum of exponentials rescaled whenever its maximum rises, the
 // threads' pairs merge, and a second pass writes -- two reads of the row
 // instead of three (max, sum, write).  Otherwise (inner > 1) one thread takes
-// an (outer, inner) position and walks dim, so that neighbouring threads read
-// neighbouring inner elements.
+// an (outer, inner) position and walks dim with the same two passes, so that
+// neighbouring threads read neighbouring inner elements.
 #include <stdint.h>
 
 #include "moe_device.h"
@@ -135,13 +135,13 @@ __global__ void __launch_bounds__(256) softmax_rows_cached_kernel(const T* __res
 // Running (maximum, sum of exponentials) of one more value; exp(-inf) = 0 on
 // a thread's first element, and -inf elements before any finite one add
 // nothing.
-template <typename A>
-__device__ __forceinline__ void sm_online(A& m, A& s, A v) {
+template <typename A, typename S>
+__device__ __forceinline__ void sm_online(A& m, S& s, A v) {
   if (v > m) {
-    s = s * sm_exp(m - v) + static_cast<A>(1);
+    s = s * static_cast<S>(sm_exp(m - v)) + static_cast<S>(1);
     m = v;
   } else if (m != -INFINITY) {
-    s += sm_exp(v - m);
+    s += static_cast<S>(sm_exp(v - m));
   }
 }
 
@@ -194,7 +194,8 @@ __global__ void __launch_bounds__(256) softmax_rows_kernel(const T* __restrict__
   }
 }
 
-// inner > 1: one thread per (outer, inner) position
+// inner > 1: one thread per (outer, inner) position, the online max-and-sum
+// pass then the write pass
 template <typename T, typename A>
 __global__ void __launch_bounds__(256) softmax_strided_kernel(const T* __restrict__ in, T* __restrict__ out,
                                                               int64_t outer, int64_t dim, int64_t inner) {
@@ -203,14 +204,12 @@ __global__ void __launch_bounds__(256) softmax_strided_kernel(const T* __restric
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t o = i / inner, j = i - o * inner;
     const int64_t base = o * dim * inner + j;
+    // one thread sums the whole axis in sequence: the sum is kept in double
+    // (the exponentials stay in A) so that its rounding does not grow with dim
     A m = -INFINITY;
-    for (int64_t d = 0; d < dim; ++d) {
-      const A v = sm_load<T, A>(in, base + d * inner);
-      m = v > m ? v : m;
-    }
-    A s = 0;
-    for (int64_t d = 0; d < dim; ++d) s += sm_exp(sm_load<T, A>(in, base + d * inner) - m);
-    const A inv = static_cast<A>(1) / s;
+    double s = 0;
+    for (int64_t d = 0; d < dim; ++d) sm_online(m, s, sm_load<T, A>(in, base + d * inner));
+    const A inv = static_cast<A>(1.0 / s);
     for (int64_t d = 0; d < dim; ++d)
       sm_store<T, A>(out, base + d * inner, sm_exp(sm_load<T, A>(in, base + d * inner) - m) * inv);
   }

@@ -67,3 +67,22 @@ def test_masked_rows(cuda, dim):
     got = y.cpu().double().numpy()
     assert np.all(np.isfinite(got))
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_masked_strided_axis(cuda):
+    # a middle axis (one thread per (outer, inner) position) with masked prefixes
+    x = np.random.default_rng(77).standard_normal((4, 500, 3)).astype(np.float32)
+    x[0, :250, :] = -np.inf
+    x[1, ::3, 1] = -np.inf
+    x[2, :-1, 2] = -np.inf
+    t = torch.from_numpy(x).to(cuda)
+    y = softmax(t, 1)
+    torch.cuda.synchronize()
+    got = y.cpu().double().numpy()
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, oracle.softmax(x.astype(np.float64), 1), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float64])
+def test_long_strided_axis(cuda, dt):
+    run(cuda, 4.0 * np.random.default_rng(78).standard_normal((16, 3000, 40)), 1, dt)
