@@ -5,7 +5,7 @@
 // (musa/ep/src/kernels/math/softmax_impl.mu:49-84).
 //
 // The input is viewed as [outer, dim, inner].  With inner == 1 one wavefront
-// takes a row, or 2 or 4 wavefronts of a workgroup share it.  Rows up to
+// takes a row, or 2, 4 or 16 wavefronts of a workgroup share it.  Rows up to
 // 16384 long stay in registers between the max, sum and write steps, so each
 // is read once.  A longer row takes a workgroup: each thread keeps a running
 // maximum and a sum of exponentials rescaled whenever its maximum rises, the
@@ -63,23 +63,22 @@ __device__ __forceinline__ A sm_wave_sum(A v) {
 }
 
 // Values per lane of the register-held rows: the smallest of 4, 16 and 32
-// that holds a row over 1, 2 or 4 waves (fewer registers, more waves per
-// SIMD), then 64 for rows of 8193..16384; 128 would pass the 256 VGPRs of a
-// wave and spill.
-constexpr int kCachedMaxNv = 64;
-// Most wavefronts sharing one register-held row (rows up to 64 * 64 * 4 =
+// that holds a row over 1, 2 or 4 waves, then 16 over 16 waves (a workgroup
+// of 1024) for rows of 8193..16384: fewer registers, more waves per SIMD
+// (64 per lane over 4 waves ran at 2 waves per SIMD).
+// Most wavefronts sharing one register-held row (rows up to 64 * 16 * 16 =
 // 16384); longer rows take softmax_rows_kernel.
-constexpr int kCachedMaxWaves = 4;
+constexpr int kCachedMaxWaves = 16;
 
 // inner == 1 and dim <= 64 NV WPR: WPR wavefronts of a workgroup take one row,
 // held in registers (NV elements per lane, d = lane + 64 (w + WPR i) for the
 // row's wave w), so it is read once: the exponentials computed for the sum
 // are the ones written.  Waves of one row combine their maxima and sums in
 // LDS.
-template <typename T, typename A, int NV, int WPR>
-__global__ void __launch_bounds__(256) softmax_rows_cached_kernel(const T* __restrict__ in, T* __restrict__ out,
-                                                                  int64_t rows, int64_t dim) {
-  __shared__ A part[2][256 / kWave];  // per-wave maximum, sum
+template <typename T, typename A, int NV, int WPR, int NT = 256>
+__global__ void __launch_bounds__(NT) softmax_rows_cached_kernel(const T* __restrict__ in, T* __restrict__ out,
+                                                                 int64_t rows, int64_t dim) {
+  __shared__ A part[2][NT / kWave];  // per-wave maximum, sum
   const int lane = threadIdx.x & 63, wave = threadIdx.x / kWave;
   const int w = wave % WPR, first = wave - w;
   const int64_t rpb = blockDim.x / kWave / WPR;
@@ -236,9 +235,9 @@ hipError_t launch_typed(const void* in, void* out, int64_t outer, int64_t dim, i
       hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 32, 2>), grid(2), block, 0, stream, x, y, outer, dim);
     else if (dim <= kWave * 32 * 4)
       hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 32, 4>), grid(1), block, 0, stream, x, y, outer, dim);
-    else if (dim <= kWave * kCachedMaxNv * kCachedMaxWaves)
-      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, kCachedMaxNv, kCachedMaxWaves>), grid(1), block, 0, stream,
-                         x, y, outer, dim);
+    else if (dim <= kWave * 16 * kCachedMaxWaves)
+      hipLaunchKernelGGL((softmax_rows_cached_kernel<T, A, 16, kCachedMaxWaves, 64 * kCachedMaxWaves>), grid(1),
+                         dim3(64 * kCachedMaxWaves), 0, stream, x, y, outer, dim);
     else
       hipLaunchKernelGGL((softmax_rows_kernel<T, A>), grid(1), block, 0, stream, x, y, outer, dim);
   } else {
