@@ -85,9 +85,6 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream);
 hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half, hipStream_t stream);
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream);
 
-// Reorders row-major quantized weights [rows, row_bytes] (rows a multiple of
-// 16, row_bytes a multiple of the chunk row bytes cbytes = 64 for int4, 128
-// for int8) into the tile-major layout read by the decode and prefill kernels.
 // ONNX TopK over the middle axis of [rows, dim, inner] (moe_topk.hip).
 struct TopKArgs {
   int64_t rows, dim, inner, k;
@@ -101,6 +98,10 @@ hipError_t launch_topk(const void* in, int32_t elem_type, void* values, int64_t*
 hipError_t launch_softmax(const void* in, void* out, int32_t elem_type, int64_t outer, int64_t dim, int64_t inner,
                           hipStream_t stream);
 
+// Reorders row-major quantized weights [rows, row_bytes] (rows a multiple of
+// 16, row_bytes a multiple of the chunk row bytes cbytes = 64 for int4, 128
+// for int8) into the tile-major layout read by the decode and prefill kernels
+// (moe_prepack.hip).
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
                           hipStream_t stream);
 
