@@ -49,6 +49,7 @@ class MoEConfig:
     alpha: float = 1.0
     beta: float = 0.0
     normalize: int = 1
+    router_sigmoid: int = 0      # library extension: sigmoid routing instead of softmax
     bias: bool = False
     router: str = "normal"       # "normal" | "zipf"
     zipf_s: float = 1.2
@@ -91,7 +92,7 @@ class MoEConfig:
     def op_kwargs(self) -> dict:
         kw = dict(k=self.k, activation_type=self.activation, normalize_routing_weights=self.normalize,
                   swiglu_fusion=self.swiglu_fusion, swiglu_limit=self.swiglu_limit,
-                  activation_alpha=self.alpha, activation_beta=self.beta)
+                  activation_alpha=self.alpha, activation_beta=self.beta, router_sigmoid=self.router_sigmoid)
         if self.bits:
             kw.update(expert_weight_bits=self.bits, block_size=self.block_size)
         return kw

@@ -14,7 +14,9 @@ from typing import Optional
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "libmoe_oracle.so"
+# MOE_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of oracle/Makefile's sanitize-test target)
+LIB = Path(os.environ.get("MOE_ORACLE_LIB") or HERE / "libmoe_oracle.so")
 
 ORC_F32, ORC_U8, ORC_F16, ORC_BF16 = 1, 2, 10, 16
 ACT = {"relu": 0, "gelu": 1, "silu": 2, "identity": 3, "swiglu": 4}
@@ -214,7 +216,8 @@ def forward_problem(cfg, host: dict, token_mask=None, threads=0):
         x=host["input"], logits=host["router_probs"], w1=host["fc1_experts_weights"],
         w2=host["fc2_experts_weights"], k=cfg.k, hidden=cfg.hidden, inter=cfg.inter, experts=cfg.experts,
         act_dtype=cfg.dtype, activation=cfg.activation, normalize=cfg.normalize, swiglu_fusion=cfg.swiglu_fusion,
-        swiglu_limit=cfg.swiglu_limit, alpha=cfg.alpha, beta=cfg.beta, bits=cfg.bits, block_size=cfg.block_size,
+        swiglu_limit=cfg.swiglu_limit, alpha=cfg.alpha, beta=cfg.beta,
+        router_sigmoid=getattr(cfg, "router_sigmoid", 0), bits=cfg.bits, block_size=cfg.block_size,
         scale_dtype=cfg.scale_dtype, s1=host.get("fc1_scales"), b1=host.get("fc1_experts_bias"),
         s2=host.get("fc2_scales"), b2=host.get("fc2_experts_bias"), w3=host.get("fc3_experts_weights"),
         s3=host.get("fc3_scales"), b3=host.get("fc3_experts_bias"), token_mask=token_mask, threads=threads)

@@ -11,9 +11,15 @@ Each oracle function is checked against something that does not restate it:
                k = 1 weight 1
   orc_dispatch brute force (a stable sort by expert) on every routing of tiny
                shapes, invariants on large random routings
-  orc_dequant  hand-packed bytes (0x80 -> 0 for int8; 0x78 -> 0, -1 for int4)
-               and block-boundary scale indexing
-  activations  closed forms at fixed points (SiLU, erf-GELU, clamped SwiGLU)
+  orc_dequant  hand-packed bytes (0x80 -> 0 for int8; 0x78 -> 0, -1 for int4),
+               block-boundary scale indexing, and a round trip through the
+               symmetric encoder written independently in float64 numpy
+               (every weight back within half a step, each row's / block's
+               peak exactly +-127 s / +-7 s, for int8/int4 x per-channel /
+               block 16/32/128 x f16/bf16/f32 scales)
+  activations  closed forms at fixed points (SiLU, erf-GELU); SwiGLU reduces
+               to textbook Swish-GLU at alpha 1, beta 0, no limit, and to
+               relu gating as alpha grows; clamp saturation of both inputs
   forward      an independent float64 numpy formulation (dense matmuls),
                layout equivalences (fc1/fc3 unfused == fused chunked ==
                fused interleaved), QMoE == MoE on dequantised weights,
@@ -21,8 +27,9 @@ Each oracle function is checked against something that does not restate it:
   fixtures     tests/golden/*.npz written by tests/golden/make_golden.py
 
 The "planted mistake" tests feed each check a plausible mistake (swapped tie
-order, unstable dispatch, high-nibble-first decode, dropped bias, swapped
-gate/linear halves) on the CPU and assert that the check rejects it.
+order, unstable dispatch, high-nibble-first decode, a zero point off by one,
+block scales along the wrong axis, dropped bias, swapped gate/linear halves)
+on the CPU and assert that the check rejects it.
 """
 import itertools
 import math
@@ -233,6 +240,100 @@ def test_dequant_f16_scales():
     assert got[0, 0] == np.float32(2.0) * np.float32(np.float16(0.1))
 
 
+# ---- quantizer round trip: the symmetric QMoE encoder as the benchmark
+# configurations specify it (int8: s = max|w| / 127, q = clamp(round(w / s),
+# -128, 127) + 128; int4: s = max|w| / 7, q = clamp(round(w / s), -8, 7) + 8,
+# two per byte, even k in the low nibble; per output channel or per block
+# along K), written here in float64 numpy with no code shared with the
+# workload generator.  Decoding what it encodes must give back every weight
+# to within half a quantisation step, and each row's (block's) largest
+# magnitude exactly as +-127 s (+-7 s).  A decoder with another zero point or
+# nibble order cannot meet that bound. ----
+_SCALE_DT = {"f32": np.float32, "f16": np.float16}
+
+
+def _store_scale(s64: np.ndarray, sdt: str):
+    """float64 scales -> (stored array for the oracle, the stored values as float64)."""
+    if sdt == "bf16":
+        bits = oracle.f32_to_bf16_bits(s64.astype(np.float32))
+        return bits, oracle.bf16_bits_to_f32(bits).astype(np.float64)
+    st = s64.astype(_SCALE_DT[sdt])
+    return st, st.astype(np.float64)
+
+
+def _spec_quantize(w: np.ndarray, bits: int, block: int, sdt: str):
+    """w [N, K] float32 -> (q uint8 [N, K*bits/8], stored scales, scales as float64 [N, K] broadcast)."""
+    N, K = w.shape
+    qmax = 127 if bits == 8 else 7
+    bs = block if block else K
+    wb = w.astype(np.float64).reshape(N, K // bs, bs)
+    s_exact = np.abs(wb).max(axis=2) / qmax                          # [N, K/bs]
+    s_store, s64 = _store_scale(s_exact if block else s_exact[:, 0], sdt)
+    s_b = (s64 if block else s64[:, None]).reshape(N, K // bs, 1)
+    v = np.clip(np.rint(wb / s_b), -qmax - 1, qmax).astype(np.int64).reshape(N, K)
+    u = (v + (qmax + 1)).astype(np.uint8)                            # zero point 128 / 8
+    q = u if bits == 8 else (u[:, 0::2] | (u[:, 1::2] << 4)).astype(np.uint8)
+    return q, s_store, np.broadcast_to(s_b, (N, K // bs, bs)).reshape(N, K)
+
+
+def _round_trip_excess(deq: np.ndarray, w: np.ndarray, s: np.ndarray) -> float:
+    """max over elements of |deq - w| / (s / 2) (1 at the exact bound)."""
+    return float(np.max(np.abs(deq.astype(np.float64) - w.astype(np.float64)) / (s / 2)))
+
+
+ROUND_TRIP_CASES = [(bits, block, sdt) for bits in (8, 4) for block in (0, 16, 32, 128)
+                    for sdt in ("f16", "bf16", "f32")]
+
+
+@pytest.mark.parametrize("bits,block,sdt", ROUND_TRIP_CASES)
+def test_quantizer_round_trip(bits, block, sdt):
+    N, K = 24, 256
+    rng = np.random.default_rng(100 + bits + block)
+    w = (rng.standard_normal((N, K)) / math.sqrt(K)).astype(np.float32)
+    # rows of different magnitude (scales stay fp16-normal: a subnormal
+    # stored scale is coarser than the encoder's rounding step)
+    w[3] *= np.float32(64.0)
+    w[5] *= np.float32(0.25)
+    q, s_store, s = _spec_quantize(w, bits, block, sdt)
+    deq = oracle.dequant(q, s_store, sdt, bits, block, N, K)
+    # every weight within half a step (plus the fp32 rounding of q * s)
+    assert _round_trip_excess(deq, w, s) <= 1.0 + 1e-5
+    # each row's / block's largest magnitude decodes to exactly +-qmax * s
+    qmax = 127 if bits == 8 else 7
+    bs = block if block else K
+    wb = w.reshape(N, K // bs, bs)
+    am = np.abs(wb).argmax(axis=2)
+    peak = np.take_along_axis(deq.reshape(N, K // bs, bs), am[..., None], 2)[..., 0]
+    sign = np.sign(np.take_along_axis(wb, am[..., None], 2)[..., 0])
+    s_blk = s.reshape(N, K // bs, bs)[..., 0].astype(np.float32)
+    np.testing.assert_array_equal(peak, sign * np.float32(qmax) * s_blk)
+
+
+@pytest.mark.parametrize("bits,block", [(8, 0), (8, 32), (4, 32), (4, 128), (4, 0)])
+def test_planted_encoding_mistakes_fail_round_trip(bits, block):
+    """The decoder is planted with plausible mistakes by feeding it altered
+    bytes or scales, which is what a decoder with that mistake would read:
+    a zero point off by one (bytes - 1: every nibble / byte is >= 1 here),
+    the high nibble first (nibbles swapped), and block scales taken along N
+    instead of K (the scale array transposed).  Each must break the bound."""
+    N, K = 16, 256
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((N, K)) / math.sqrt(K)).astype(np.float32)
+    q, s_store, s = _spec_quantize(w, bits, block, "f32")
+    good = oracle.dequant(q, s_store, "f32", bits, block, N, K)
+    assert _round_trip_excess(good, w, s) <= 1.0 + 1e-5
+    mutants = {"zero point off by one": (q - (0x11 if bits == 4 else 1)).astype(np.uint8)}
+    if bits == 4:
+        mutants["high nibble first"] = (((q & 0x0F) << 4) | (q >> 4)).astype(np.uint8)
+    for what, qm in mutants.items():
+        bad = oracle.dequant(qm, s_store, "f32", bits, block, N, K)
+        assert _round_trip_excess(bad, w, s) > 1.5, what
+    if block:
+        st = np.ascontiguousarray(s_store.reshape(N, K // block).T).reshape(N, K // block)
+        bad = oracle.dequant(q, st, "f32", bits, block, N, K)
+        assert _round_trip_excess(bad, w, s) > 1.5, "block scales along N"
+
+
 # ---------------------------------------------------------------- activations
 def test_activation_closed_forms():
     h = np.array([1.0, -2.0, 0.5], np.float32)
@@ -262,6 +363,56 @@ def test_swiglu_layouts_and_clamp():
     np.testing.assert_allclose(oracle.activation(g, l, 2, "swiglu", 0, alpha, beta, lim), ref(g, l), rtol=1e-6)
     # SiLU gating with fc3
     np.testing.assert_allclose(oracle.activation(g, l, 2, "silu"), g / (1 + np.exp(-g)) * l, rtol=1e-6)
+
+
+def _silu64(g):
+    g = np.asarray(g, np.float64)
+    return g / (1.0 + np.exp(-g))
+
+
+def test_swiglu_reduces_to_textbook_swish_glu():
+    """alpha = 1, beta = 0, no limit: SwiGLU(g, l) = Swish_1(g) * l, the GLU
+    variant of Shazeer, "GLU Variants Improve Transformer" (2020), eq. 6."""
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal(64) * 4).astype(np.float32)
+    l = (rng.standard_normal(64) * 4).astype(np.float32)
+    exp = _silu64(g) * l.astype(np.float64)
+    for fusion, h1, h3 in [(0, g, l), (1, np.stack([g, l], 1).reshape(-1), None), (2, np.concatenate([g, l]), None)]:
+        got = oracle.activation(h1, h3, 64, "swiglu", fusion, 1.0, 0.0, float("inf"))
+        np.testing.assert_allclose(got, exp, rtol=2e-6, atol=1e-7)
+
+
+def test_swiglu_large_alpha_gates_like_relu():
+    """sigma(alpha g) tends to the step function as alpha grows, so
+    g * sigma(alpha g) * (l + beta) tends to relu(g) * (l + beta)."""
+    g = np.array([-3.0, -0.5, 0.5, 3.0], np.float32)
+    l = np.array([1.5, -2.0, 0.25, -0.75], np.float32)
+    got = oracle.activation(g, l, 4, "swiglu", 0, 1e4, 1.0, float("inf"))
+    np.testing.assert_allclose(got, np.maximum(g, 0) * (l + 1.0), rtol=1e-6, atol=1e-30)
+
+
+def test_swiglu_clamp_saturation():
+    """With a limit: a gate at or above it gives the same output whatever its
+    value (one-sided: a gate below -limit is not clamped), a linear input is
+    clamped on both sides, and beta is added after the clamp (the form of
+    the published gpt-oss SwiGLU, openai/gpt-oss, which this config mirrors)."""
+    lim, alpha, beta = 7.0, 1.702, 1.0
+
+    def one(g, l):
+        return float(oracle.activation(np.array([g], np.float32), np.array([l], np.float32), 1, "swiglu", 0,
+                                       alpha, beta, lim)[0])
+
+    at = one(lim, 0.5)
+    for g in (7.25, 50.0, 1e30, np.inf):
+        assert one(g, 0.5) == at
+    assert one(-7.5, 0.5) != one(-8.0, 0.5)                # no clamp below -limit for the gate
+    assert one(2.0, 9.0) == one(2.0, lim) and one(2.0, -40.0) == one(2.0, -lim)
+    assert one(2.0, 6.0) != one(2.0, lim)                  # below the limit nothing is clamped
+    # beta after the clamp: l = 6.5 gives (6.5 + 1), not clamp(7.5) = 7
+    np.testing.assert_allclose(one(2.0, 6.5), float(2.0 / (1 + np.exp(-alpha * 2.0)) * 7.5), rtol=1e-6)
+    # and beta is a shift of the linear input below the limit
+    assert one(2.0, 3.0) == float(oracle.activation(np.array([2.0], np.float32), np.array([4.0], np.float32), 1,
+                                                    "swiglu", 0, alpha, 0.0, lim)[0])
 
 
 def test_planted_swapped_gate_linear_is_caught():
