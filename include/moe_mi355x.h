@@ -37,6 +37,17 @@
  * be called concurrently from several threads on different streams when each
  * call passes its own workspace.  With workspace == NULL the kernel uses a
  * workspace it caches per (device, stream), guarded by a mutex.
+ *
+ * Debugging (read from the environment when a kernel is created, the role of
+ * the reference's MUSA_EP_TRACE_KERNELS / MUSA_EP_TRACE_SYNC,
+ * musa/ep/src/kernels/shared_inc/kernel_base.h:48-80):
+ *   MOE_TRACE_KERNELS=1  one MOE_KERNEL_BEGIN and one MOE_KERNEL_END line per
+ *                        moe_kernel_compute call on stderr (the end line
+ *                        carries the path and the status);
+ *   MOE_DEBUG_SYNC=1     moe_kernel_compute waits for its stream after each
+ *                        stage and returns MOE_EP_FAIL naming the first stage
+ *                        that failed (this breaks the no-synchronisation
+ *                        promise below on purpose).
  */
 #ifndef MOE_MI355X_H_
 #define MOE_MI355X_H_
@@ -128,8 +139,15 @@ MOE_API moe_status moe_kernel_workspace_size(const moe_kernel *kernel, const moe
                                      int32_t num_inputs, size_t *bytes);
 
 /* Runs the op: output is a device buffer of the input's shape and type.
- * All work is enqueued on `stream`; no host synchronisation, no device->host
- * reads.  workspace may be NULL (cached internal workspace). */
+ * All work is enqueued on `stream`; no device->host reads.  With a caller
+ * workspace (at least moe_kernel_workspace_size bytes) the call allocates
+ * nothing and does not synchronise.  workspace may be NULL: the kernel then
+ * uses a workspace it caches per (device, stream).  The first call on a
+ * (device, stream) allocates it (hipMalloc), and a later call that needs a
+ * larger one waits for the stream (hipStreamSynchronize), frees the old
+ * buffer and allocates a new one; calls that fit the cached size neither
+ * allocate nor synchronise.  A caller that must not block passes a workspace
+ * sized for its largest batch. */
 MOE_API moe_status moe_kernel_compute(const moe_kernel *kernel, const moe_tensor *inputs,
                               int32_t num_inputs, void *output, void *workspace,
                               size_t workspace_bytes, void *stream);
@@ -182,8 +200,11 @@ MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
  *   caller may then pass data == NULL for it (its shape is taken from the
  *   packed tensor) or the same tensor (shape checked).  dst must stay valid
  *   while the kernel lives; the source may be freed once the stream has run
- *   the pack.  fc1 and fc3 are packed together or not at all.  Call before
- *   the kernel is shared between threads. */
+ *   the pack.  A later call that passes a tensor for a packed input must
+ *   pass the one that was packed (same data pointer) or dst itself;
+ *   another tensor, even of the same shape, is MOE_INVALID_ARGUMENT.  fc1
+ *   and fc3 are packed together or not at all.  Call before the kernel is
+ *   shared between threads. */
 MOE_API moe_status moe_kernel_prepack_size(const moe_kernel *kernel, int32_t input_index,
                                            const moe_tensor *weights, int32_t act_type, size_t *bytes);
 MOE_API moe_status moe_kernel_prepack(moe_kernel *kernel, int32_t input_index, const moe_tensor *weights,
@@ -238,14 +259,16 @@ MOE_API moe_status moe_route_dispatch_launch(const moe_route_params *params, voi
  * order).  The input is viewed as [rows, dim, inner] with the axis in the
  * middle; values [rows, k, inner] keep the input's type, indices are int64.
  * Types: float, float16, bfloat16, double, int32, int64.  -0.0 ties with
- * +0.0; NaN sorts above +inf.  Replaces the reference's TopK kernel launchers
+ * +0.0; every NaN (either sign, any payload) sorts above +inf, NaNs tied
+ * with each other.  Any axis length; k up to 8192 on axes longer than 8192
+ * (radix select), any k on shorter ones.  Replaces the reference's TopK kernel launchers
  * LaunchMusaTopK{PairReduce,BlockSort,...}Kernel(input, values, indices,
  * MusaTopKParams{rows, dim, inner, k, largest, sorted}, elem_type, stream)
  * (musa/ep/src/kernels/math/topk_impl.h:10-33,
  * shared_inc/device_kernel_types.h:258-266) and their validation
  * (musa/ep/src/kernels/math/topk.cc:133-200): k outside [0, dim] ->
- * MOE_INVALID_ARGUMENT, an unsupported type or dim > 8192 ->
- * MOE_NOT_IMPLEMENTED. */
+ * MOE_INVALID_ARGUMENT, an unsupported type, or k > 8192 on an axis
+ * longer than 8192 -> MOE_NOT_IMPLEMENTED. */
 typedef struct moe_topk_params {
   const void *input;
   int32_t elem_type; /* moe_elem_type */

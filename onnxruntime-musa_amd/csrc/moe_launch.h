@@ -91,6 +91,9 @@ struct TopKArgs {
   int32_t largest, sorted;
 };
 constexpr int64_t kTopKMaxDim = 8192;  // one workgroup sorts a slice in LDS
+// Longer axes: radix select, then a sort of the k winners in LDS.
+constexpr int64_t kTopKRadixMaxK = 8192;
+constexpr int64_t kTopKRadixMaxDim = (int64_t{1} << 31) - 1;  // 32-bit indices in LDS
 hipError_t launch_topk(const void* in, int32_t elem_type, void* values, int64_t* indices, const TopKArgs& p,
                        hipStream_t stream);
 

@@ -21,6 +21,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <limits>
@@ -111,9 +113,15 @@ struct moe_kernel {
   hipEvent_t ev[5] = {};
   bool ev_recorded = false;
   int32_t last_path = -1;
+  // debug switches, read from the environment at creation (the role of the
+  // reference's MUSA_EP_TRACE_KERNELS / MUSA_EP_TRACE_SYNC,
+  // musa/ep/src/kernels/shared_inc/kernel_base.h:48-80): trace prints a
+  // begin and an end line per call to stderr; debug_sync waits for the
+  // stream after each stage and turns a failure into MOE_EP_FAIL naming it
+  bool trace = false, debug_sync = false;
   // Pre-packed (tile-major) expert weights by QMoE input index (2 fc1, 5
   // fc2, 8 fc3): the caller-owned device copy and the tensor it was packed
-  // from (shape and type; its data pointer is not kept).
+  // from (shape, type and data pointer).
   struct Packed {
     const void* data = nullptr;
     moe_tensor src{};
@@ -269,8 +277,10 @@ moe_status validate(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, P
 }
 
 // Inputs of one call with pre-packed weights in place of theirs: a packed
-// input may come with data == NULL (shape taken from the packed tensor) or
-// with a descriptor that must match the tensor that was packed.
+// input may come with data == NULL (shape taken from the packed tensor), or
+// as the tensor that was packed (same data pointer, shape and type) or the
+// packed copy itself.  Any other tensor is an error: the kernel would compute
+// with the weights it packed, not with the ones given.
 moe_status with_packed(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, moe_tensor* local) {
   for (int32_t i = 0; i < n; ++i) local[i] = inputs[i];
   for (int32_t i = 0; i < n && i < 11; ++i) {
@@ -282,12 +292,21 @@ moe_status with_packed(const moe_kernel* kr, const moe_tensor* inputs, int32_t n
       if (!same)
         return fail(MOE_INVALID_ARGUMENT, "input " + std::to_string(i) + " " + dims_str(inputs[i]) +
                                               " differs from the pre-packed weights " + dims_str(pk.src));
+      if (inputs[i].data != pk.src.data && inputs[i].data != pk.data)
+        return fail(MOE_INVALID_ARGUMENT, "input " + std::to_string(i) +
+                                              " is not the tensor that was pre-packed (another data pointer); "
+                                              "pass that tensor, its packed copy or NULL");
     } else {
       local[i] = pk.src;
     }
     local[i].data = pk.data;
   }
   return MOE_OK;
+}
+
+bool env_set(const char* name) {
+  const char* v = std::getenv(name);
+  return v && *v && std::strcmp(v, "0") != 0;
 }
 
 // Bytes of the tile-major copy of QMoE weight input idx, or 0 when the
@@ -446,6 +465,8 @@ moe_status moe_kernel_create(const char* op_type, const moe_attributes* attrs, m
     auto* k = new moe_kernel();
     k->quantized = q;
     k->attrs = a;
+    k->trace = env_set("MOE_TRACE_KERNELS");
+    k->debug_sync = env_set("MOE_DEBUG_SYNC");
     *out = k;
     return MOE_OK;
   } catch (const std::exception& e) {
@@ -490,7 +511,6 @@ moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe
     if (e != hipSuccess) return hip_fail(e, "pre-pack launch");
     kernel->packed[input_index].data = dst;
     kernel->packed[input_index].src = *weights;
-    kernel->packed[input_index].src.data = nullptr;
     *is_packed = 1;
     return MOE_OK;
   } catch (const std::exception& e) {
@@ -543,10 +563,13 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
   }
 }
 
-moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
-                              void* workspace, size_t workspace_bytes, void* stream_ptr) {
+}  // extern "C"
+
+namespace {
+
+moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
+                        void* workspace, size_t workspace_bytes, void* stream_ptr) {
   try {
-    if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
     if (!inputs || n < 0 || n > 64) return fail(MOE_INVALID_ARGUMENT, "bad inputs");
     moe_tensor local[64];
     moe_status st = with_packed(kernel, inputs, n, local);
@@ -617,35 +640,54 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     auto mark = [&](int i) {
       if (prof && e == hipSuccess) e = hipEventRecord(mk->ev[i], stream);
     };
+    // MOE_DEBUG_SYNC: wait for each stage and report the first that fails
+    const char* failed_stage = nullptr;
+    auto stage_done = [&](const char* name) {
+      if (!kernel->debug_sync || e != hipSuccess) return;
+      e = hipStreamSynchronize(stream);
+      if (e == hipSuccess) e = hipGetLastError();
+      if (e != hipSuccess) failed_stage = name;
+    };
     // small decode batches are routed inside the fc1 kernel (one launch less)
     const bool route_in_fc1 = path == moe::kPathDecode && moe::decode_routes_in_fc1(a);
     mark(0);
     if (!route_in_fc1) {
       e = e == hipSuccess ? moe::launch_route_dispatch(ra, stream) : e;
       if (e != hipSuccess) return hip_fail(e, "router/dispatch launch");
+      stage_done("router/dispatch");
     }
     mark(1);
     switch (path) {
       case moe::kPathDecode:
-        e = moe::launch_fc1_decode(a, route_in_fc1 ? &ra.p : nullptr, stream);
+        e = e == hipSuccess ? moe::launch_fc1_decode(a, route_in_fc1 ? &ra.p : nullptr, stream) : e;
+        stage_done("fc1 (decode)");
         mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_decode(a, &a.y2_planes, stream);
+        stage_done("fc2 (decode)");
         break;
       case moe::kPathPrefill:
-        e = moe::launch_fc1_prefill(a, stream);
+        e = e == hipSuccess ? moe::launch_fc1_prefill(a, stream) : e;
+        stage_done("fc1 (prefill)");
         mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_prefill(a, &a.y2_planes, &a.y2_half, stream);
+        stage_done("fc2 (prefill)");
         break;
       default:
-        e = moe::launch_fc1_simt(a, stream);
+        e = e == hipSuccess ? moe::launch_fc1_simt(a, stream) : e;
+        stage_done("fc1 (simt)");
         mark(2);
         if (e == hipSuccess) e = moe::launch_fc2_simt(a, stream);
+        stage_done("fc2 (simt)");
         break;
     }
-    if (e != hipSuccess) return hip_fail(e, "expert launch");
+    if (e != hipSuccess)
+      return hip_fail(e, failed_stage ? (std::string("stage ") + failed_stage + " (MOE_DEBUG_SYNC)").c_str()
+                                      : "expert launch");
     mark(3);
     e = moe::launch_finalize(a, stream);
     if (e != hipSuccess) return hip_fail(e, "finalize launch");
+    stage_done("finalize");
+    if (e != hipSuccess) return hip_fail(e, "stage finalize (MOE_DEBUG_SYNC)");
     mark(4);
     if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
     mk->last_path = path;
@@ -656,6 +698,28 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
   } catch (const std::exception& e) {
     return fail(MOE_FAIL, e.what());
   }
+}
+
+}  // namespace
+
+extern "C" {
+
+moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
+                              void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+  if (kernel->trace) {
+    std::fprintf(stderr, "MOE_KERNEL_BEGIN %s kernel=%p\n", kernel->quantized ? "QMoE" : "MoE",
+                 static_cast<const void*>(kernel));
+    std::fflush(stderr);
+  }
+  const moe_status st = compute_impl(kernel, inputs, n, output, workspace, workspace_bytes, stream_ptr);
+  if (kernel->trace) {
+    std::fprintf(stderr, "MOE_KERNEL_END %s kernel=%p path=%d status=%d%s%s\n", kernel->quantized ? "QMoE" : "MoE",
+                 static_cast<const void*>(kernel), kernel->last_path, static_cast<int>(st),
+                 st == MOE_OK ? "" : " ", st == MOE_OK ? "" : g_last_error.c_str());
+    std::fflush(stderr);
+  }
+  return st;
 }
 
 void moe_kernel_release(moe_kernel* kernel) { delete kernel; }
@@ -705,8 +769,10 @@ moe_status moe_topk_launch(const moe_topk_params* p, void* stream) {
       default: return fail(MOE_NOT_IMPLEMENTED, "TopK unsupported dtype");
     }
     if (p->rows * p->inner == 0 || p->k == 0) return MOE_OK;
-    if (p->dim > moe::kTopKMaxDim)
-      return fail(MOE_NOT_IMPLEMENTED, "TopK axis longer than " + std::to_string(moe::kTopKMaxDim));
+    if (p->dim > moe::kTopKMaxDim && (p->k > moe::kTopKRadixMaxK || p->dim > moe::kTopKRadixMaxDim))
+      return fail(MOE_NOT_IMPLEMENTED, "TopK with k > " + std::to_string(moe::kTopKRadixMaxK) +
+                                           " on an axis longer than " + std::to_string(moe::kTopKMaxDim) +
+                                           " (or an axis of 2^31 or more)");
     if (!p->input || !p->values || !p->indices) return fail(MOE_INVALID_ARGUMENT, "null tensor");
     const moe::TopKArgs a{p->rows, p->dim, p->inner, p->k, p->largest, p->sorted};
     const hipError_t e = moe::launch_topk(p->input, p->elem_type, p->values, p->indices, a,

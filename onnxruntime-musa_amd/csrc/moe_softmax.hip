@@ -133,13 +133,15 @@ __global__ void __launch_bounds__(NT) softmax_rows_cached_kernel(const T* __rest
 
 // Running (maximum, sum of exponentials) of one more value; exp(-inf) = 0 on
 // a thread's first element, and -inf elements before any finite one add
-// nothing.
+// nothing.  A NaN makes the sum NaN wherever it arrives (it compares false
+// with the maximum, so it is caught by the second test), so that its row
+// comes out all NaN like the register-held kernels'.
 template <typename A, typename S>
 __device__ __forceinline__ void sm_online(A& m, S& s, A v) {
   if (v > m) {
     s = s * static_cast<S>(sm_exp(m - v)) + static_cast<S>(1);
     m = v;
-  } else if (m != -INFINITY) {
+  } else if (m != -INFINITY || v != v) {
     s += static_cast<S>(sm_exp(v - m));
   }
 }

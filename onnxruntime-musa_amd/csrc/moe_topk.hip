@@ -15,8 +15,13 @@
 // bitonic network sorts (key desc, index asc).  The first k entries are written out; values are read
 // back from the input at their index, so they keep their exact bits.
 //
-// NaN keys sort as the largest values (above +inf) for largest = 1 and the
-// smallest for largest = 0.
+// Axes longer than 8192 (k <= 8192) take a radix select instead
+// (topk_radix_kernel): the k-th key is found digit by digit, the k winners
+// are collected and only they are sorted.
+//
+// Every NaN (either sign, any payload) has one key, above +inf: NaNs sort as
+// the largest values for largest = 1 and the smallest for largest = 0, tied
+// with each other (so in index order).
 #include <stdint.h>
 
 #include <type_traits>
@@ -31,7 +36,8 @@ template <typename T>
 __device__ __forceinline__ uint64_t topk_key(T v);
 // floats: flip all bits of negatives, set the sign bit of positives
 __device__ __forceinline__ uint64_t key_f64(double d) {
-  if (d == 0.0) d = 0.0;  // -0.0 ties with +0.0
+  if (d == 0.0) d = 0.0;                          // -0.0 ties with +0.0
+  if (d != d) return uint64_t{0xFFF8000000000000};  // every NaN: the key of +qNaN
   const uint64_t b = __builtin_bit_cast(uint64_t, d);
   return (b >> 63) ? ~b : (b | (uint64_t{1} << 63));
 }
@@ -58,6 +64,30 @@ __device__ __forceinline__ bool entry_before(uint64_t ka, uint32_t ia, uint64_t 
   return ka > kb || (ka == kb && ia < ib);
 }
 
+// Bitonic network over n (a power of two) LDS entries: segments of `size`
+// alternate direction until the last merge, which leaves (key desc, index
+// asc).  Every thread of the workgroup calls it; it ends on a barrier.
+template <typename KT>
+__device__ void bitonic_lds(KT* key, uint32_t* idx, int n, int tid, int nt) {
+  for (int size = 2; size <= n; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int q = tid; q < (n >> 1); q += nt) {
+        const int lo = 2 * stride * (q / stride) + (q % stride), hi = lo + stride;
+        const bool up = (lo & size) == 0;
+        const KT kl = key[lo], kh = key[hi];
+        const uint32_t il = idx[lo], ih = idx[hi];
+        if ((kh > kl || (kh == kl && ih < il)) == up) {
+          key[lo] = kh;
+          key[hi] = kl;
+          idx[lo] = ih;
+          idx[hi] = il;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T* __restrict__ values,
                                                     int64_t* __restrict__ indices, TopKArgs p, int n) {
@@ -80,25 +110,7 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
       }
     }
     __syncthreads();
-    // bitonic network: segments of `size` alternate direction until the
-    // last merge, which leaves (key desc, index asc)
-    for (int size = 2; size <= n; size <<= 1) {
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        for (int q = tid; q < (n >> 1); q += nt) {
-          const int lo = 2 * stride * (q / stride) + (q % stride), hi = lo + stride;
-          const bool up = (lo & size) == 0;
-          const uint64_t kl = key[lo], kh = key[hi];
-          const uint32_t il = idx[lo], ih = idx[hi];
-          if (entry_before(kh, ih, kl, il) == up) {
-            key[lo] = kh;
-            key[hi] = kl;
-            idx[lo] = ih;
-            idx[hi] = il;
-          }
-        }
-        __syncthreads();
-      }
-    }
+    bitonic_lds(key, idx, n, tid, nt);
     for (int64_t j = tid; j < p.k; j += nt) {
       const uint32_t s = idx[j];
       const int64_t o = (row * p.k + j) * p.inner + in0;
@@ -116,7 +128,8 @@ __global__ void __launch_bounds__(1024) topk_kernel(const T* __restrict__ in, T*
 // keep a (key, index) pair.  A retired or absent entry is dead(), after every
 // live one.
 __device__ __forceinline__ uint32_t key_f32(float f) {
-  if (f == 0.0f) f = 0.0f;  // -0.0 ties with +0.0
+  if (f == 0.0f) f = 0.0f;            // -0.0 ties with +0.0
+  if (f != f) return 0xFFC00000u;     // every NaN: the key of +qNaN
   const uint32_t b = __builtin_bit_cast(uint32_t, f);
   return (b >> 31) ? ~b : (b | 0x80000000u);
 }
@@ -311,6 +324,134 @@ __global__ void __launch_bounds__(256) topk_block_kernel(const T* __restrict__ i
   }
 }
 
+// Axes longer than 8192 with k <= 8192: one workgroup of 1024 threads per
+// slice.  A most-significant-digit radix select finds the k-th key: for each
+// 8-bit digit, from the top, a 256-bin LDS histogram counts the keys that
+// share the digits fixed so far (one read of the slice per digit) and the
+// digit holding the k-th key is fixed.  The key it ends on, thr, is the k-th
+// key; `need` keys equal to it belong to the output.  A collection pass then
+// puts every key above thr into LDS (atomic positions: they are sorted
+// afterwards) and the `need` lowest-index keys equal to thr (ranked in index
+// order with wave ballots, tile by tile), and the bitonic network sorts
+// those k entries.  Keys are those of the register kernels (32-bit for
+// elements of 32 bits or less), so the order is the same as theirs.
+template <typename T>
+__device__ __forceinline__ auto radix_key(T v) {
+  if constexpr (sizeof(T) <= 4) return Packed<T>::key(v);
+  else return topk_key<T>(v);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(1024) topk_radix_kernel(const T* __restrict__ in, T* __restrict__ values,
+                                                          int64_t* __restrict__ indices, TopKArgs p, int n) {
+  using KT = std::conditional_t<sizeof(T) <= 4, uint32_t, uint64_t>;
+  constexpr int kBits = 8 * static_cast<int>(sizeof(KT));
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  KT* lkey = reinterpret_cast<KT*>(smem);
+  uint32_t* lidx = reinterpret_cast<uint32_t*>(smem + static_cast<size_t>(n) * sizeof(KT));
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t wcnt[1024 / kWave];
+  __shared__ uint32_t s_digit, s_need, s_gt;
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid / kWave, nw = nt / kWave;
+  const int64_t slices = p.rows * p.inner, dim = p.dim;
+  const uint32_t k = static_cast<uint32_t>(p.k);
+  const bool largest = p.largest != 0;
+  for (int64_t sl = blockIdx.x; sl < slices; sl += gridDim.x) {  // uniform per workgroup
+    const int64_t row = sl / p.inner, in0 = sl - row * p.inner;
+    const T* src = in + row * p.dim * p.inner + in0;
+    auto key_at = [&](int64_t i) -> KT {
+      const KT kv = radix_key<T>(src[i * p.inner]);
+      return largest ? kv : static_cast<KT>(~kv);
+    };
+    // ---- radix select: prefix holds the digits fixed so far (mask marks
+    // them); need = how many of the keys matching prefix still belong to
+    // the output ----
+    KT prefix = 0, mask = 0;
+    uint32_t need = k;
+    for (int shift = kBits - 8; shift >= 0; shift -= 8) {
+      for (int b = tid; b < 256; b += nt) hist[b] = 0;
+      __syncthreads();
+      for (int64_t i = tid; i < dim; i += nt) {
+        const KT kv = key_at(i);
+        if ((kv & mask) == prefix) atomicAdd(&hist[static_cast<uint32_t>(kv >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        // the largest digit d with (keys of digits above d) < need <= (keys of digits >= d)
+        uint32_t above = 0;
+        int d = 255;
+        for (; d > 0; --d) {
+          if (above + hist[d] >= need) break;
+          above += hist[d];
+        }
+        s_digit = static_cast<uint32_t>(d);
+        s_need = need - above;
+      }
+      __syncthreads();
+      prefix |= static_cast<KT>(s_digit) << shift;
+      mask |= static_cast<KT>(255) << shift;
+      need = s_need;
+    }
+    // ---- collection: the k - need keys above thr, then the need
+    // lowest-index keys equal to it ----
+    const KT thr = prefix;
+    const uint32_t ngt = k - need;
+    if (tid == 0) s_gt = 0;
+    __syncthreads();
+    uint32_t taken = 0;  // keys equal to thr seen in earlier tiles (uniform)
+    for (int64_t base = 0; base < dim; base += nt) {
+      const int64_t i = base + tid;
+      KT kv = 0;
+      bool gt = false, eq = false;
+      if (i < dim) {
+        kv = key_at(i);
+        gt = kv > thr;
+        eq = kv == thr;
+      }
+      if (gt) {
+        const uint32_t pos = atomicAdd(&s_gt, 1u);
+        lkey[pos] = kv;
+        lidx[pos] = static_cast<uint32_t>(i);
+      }
+      const uint64_t bal = __ballot(eq);
+      const uint32_t before = static_cast<uint32_t>(__popcll(bal & ((uint64_t{1} << lane) - 1)));
+      if (lane == 0) wcnt[wave] = static_cast<uint32_t>(__popcll(bal));
+      __syncthreads();
+      // between the barriers every gt position of this tile is taken and no
+      // thread takes one of the next tile: the same count for all threads
+      const uint32_t gt_seen = s_gt;
+      uint32_t woff = 0, tot = 0;
+      for (int w = 0; w < nw; ++w) {
+        const uint32_t c = wcnt[w];
+        woff += w < wave ? c : 0;
+        tot += c;
+      }
+      const uint32_t r = taken + woff + before;
+      if (eq && r < need) {
+        lkey[ngt + r] = kv;
+        lidx[ngt + r] = static_cast<uint32_t>(i);
+      }
+      taken += tot;
+      __syncthreads();  // wcnt and s_gt are read before the next tile
+      if (taken >= need && gt_seen == ngt) break;  // uniform: every winner is in LDS
+    }
+    // padding entries sort after every real one (key 0, the largest index)
+    for (int j = static_cast<int>(k) + tid; j < n; j += nt) {
+      lkey[j] = 0;
+      lidx[j] = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    bitonic_lds(lkey, lidx, n, tid, nt);
+    for (int j = tid; j < static_cast<int>(k); j += nt) {
+      const uint32_t s = lidx[j];
+      const int64_t o = (row * p.k + j) * p.inner + in0;
+      values[o] = src[static_cast<int64_t>(s) * p.inner];
+      indices[o] = static_cast<int64_t>(s);
+    }
+    __syncthreads();  // LDS is reused by the next slice
+  }
+}
+
 template <typename T>
 hipError_t launch_typed(const void* in, void* values, int64_t* indices, const TopKArgs& p, hipStream_t stream) {
   const int64_t slices = p.rows * p.inner;
@@ -342,6 +483,16 @@ hipError_t launch_typed(const void* in, void* values, int64_t* indices, const To
       hipLaunchKernelGGL((topk_block_kernel<T, 16>), grid, dim3(256), 0, stream, x, v, indices, p);
     else
       hipLaunchKernelGGL((topk_block_kernel<T, 32>), grid, dim3(256), 0, stream, x, v, indices, p);
+    return hipGetLastError();
+  }
+  if (p.dim > kTopKMaxDim) {
+    // radix select (the host checks k <= kTopKRadixMaxK, dim < 2^31)
+    int n = 2;
+    while (n < p.k) n <<= 1;
+    const size_t kbytes = sizeof(T) <= 4 ? 4 : 8;
+    const unsigned grid = static_cast<unsigned>(slices < (int64_t{1} << 20) ? slices : (int64_t{1} << 20));
+    hipLaunchKernelGGL(topk_radix_kernel<T>, dim3(grid), dim3(1024), static_cast<size_t>(n) * (kbytes + 4), stream,
+                       static_cast<const T*>(in), static_cast<T*>(values), indices, p, n);
     return hipGetLastError();
   }
   int n = 1;

@@ -108,8 +108,9 @@ class _MoEOp:
                                                 ctypes.byref(nb)))
         if nb.value == 0:
             return None
-        dst = torch.empty((nb.value,), dtype=torch.uint8, device=weights.device)
         s = stream if stream is not None else torch.cuda.current_stream(weights.device)
+        with torch.cuda.stream(s):
+            dst = torch.empty((nb.value,), dtype=torch.uint8, device=weights.device)
         packed = ctypes.c_int32()
         check(self._lib.moe_kernel_prepack(self._h, int(input_index), ctypes.byref(d), _ELEM[act_dtype],
                                            ctypes.c_void_p(dst.data_ptr()), nb.value, ctypes.c_void_p(s.cuda_stream),
@@ -167,11 +168,12 @@ class _MoEOp:
                  stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         arr, n = self._descs(inputs)
         x = inputs[0]
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
         if out is None:
-            out = torch.empty_like(x)
+            with torch.cuda.stream(s):  # the caching allocator ties the block to the launch stream
+                out = torch.empty_like(x)
         elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError("out must match the input's shape and dtype")
-        s = stream if stream is not None else torch.cuda.current_stream(x.device)
         ws_ptr, ws_bytes = None, 0
         if workspace is not None:
             ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
@@ -219,15 +221,20 @@ def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoi
         raise ValueError("logits must be [T, E]")
     T, E = logits.shape
     dev = logits.device
-    res = {
-        "topk_ids": torch.empty((T, k), dtype=torch.int32, device=dev),
-        "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
-        "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
-        "perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
-        "inv_perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
-    }
+    s = stream if stream is not None else torch.cuda.current_stream(dev)
     nscratch = lib.moe_route_dispatch_scratch_size(T, E, k)
-    scratch = torch.empty((max(nscratch, 1),), dtype=torch.uint8, device=dev)
+    # results and scratch are allocated on the launch stream: the caching
+    # allocator then reuses the scratch block (freed on return) only for work
+    # ordered after this launch on that stream
+    with torch.cuda.stream(s):
+        res = {
+            "topk_ids": torch.empty((T, k), dtype=torch.int32, device=dev),
+            "topk_w": torch.empty((T, k), dtype=torch.float32, device=dev),
+            "offsets": torch.empty((E + 1,), dtype=torch.int32, device=dev),
+            "perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
+            "inv_perm": torch.empty((T * k,), dtype=torch.int32, device=dev),
+        }
+        scratch = torch.empty((max(nscratch, 1),), dtype=torch.uint8, device=dev)
     p = MoeRouteParams()
     p.logits = logits.data_ptr() if logits.numel() else None
     p.logits_type = _ELEM[logits.dtype]
@@ -238,7 +245,6 @@ def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoi
         setattr(p, name, res[name].data_ptr() if res[name].numel() else None)
     p.scratch = scratch.data_ptr()
     p.scratch_bytes = nscratch
-    s = stream if stream is not None else torch.cuda.current_stream(dev)
     check(lib.moe_route_dispatch_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
     return res
 
@@ -268,8 +274,10 @@ def topk(x: torch.Tensor, k: int, axis: int = -1, largest: int = 1, sorted: int 
     for d in shape[ax + 1:]:
         inner *= d
     out_shape = shape[:ax] + [max(int(k), 0)] + shape[ax + 1:]
-    values = torch.empty(out_shape, dtype=x.dtype, device=x.device)
-    indices = torch.empty(out_shape, dtype=torch.int64, device=x.device)
+    s = stream if stream is not None else torch.cuda.current_stream(x.device)
+    with torch.cuda.stream(s):
+        values = torch.empty(out_shape, dtype=x.dtype, device=x.device)
+        indices = torch.empty(out_shape, dtype=torch.int64, device=x.device)
     p = MoeTopKParams()
     p.input = x.data_ptr() if x.numel() else None
     p.elem_type = _TOPK_ELEM.get(x.dtype, 0)
@@ -277,7 +285,6 @@ def topk(x: torch.Tensor, k: int, axis: int = -1, largest: int = 1, sorted: int 
     p.rows, p.dim, p.inner, p.k = rows, shape[ax], inner, int(k)
     p.values = values.data_ptr() if values.numel() else None
     p.indices = indices.data_ptr() if indices.numel() else None
-    s = stream if stream is not None else torch.cuda.current_stream(x.device)
     check(lib.moe_topk_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
     return values, indices
 
@@ -299,13 +306,14 @@ def softmax(x: torch.Tensor, axis: int = -1, stream: Optional[torch.cuda.Stream]
     inner = 1
     for d in x.shape[ax + 1:]:
         inner *= d
-    y = torch.empty_like(x)
+    s = stream if stream is not None else torch.cuda.current_stream(x.device)
+    with torch.cuda.stream(s):
+        y = torch.empty_like(x)
     p = MoeSoftmaxParams()
     p.input = x.data_ptr() if x.numel() else None
     p.output = y.data_ptr() if y.numel() else None
     p.elem_type = _TOPK_ELEM.get(x.dtype, 0) if x.dtype.is_floating_point else 0
     p.outer, p.dim, p.inner = outer, x.shape[ax], inner
-    s = stream if stream is not None else torch.cuda.current_stream(x.device)
     check(lib.moe_softmax_launch(ctypes.byref(p), ctypes.c_void_p(s.cuda_stream)))
     return y
 

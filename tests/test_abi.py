@@ -376,7 +376,8 @@ def topk_status(lib, **kw):
     (dict(largest=2), C.MOE_INVALID_ARGUMENT),     # topk.cc:143-150
     (dict(sorted=3), C.MOE_INVALID_ARGUMENT),
     (dict(elem_type=C.ELEM_UINT8), C.MOE_NOT_IMPLEMENTED),  # topk.cc:179-183
-    (dict(dim=8193, k=3), C.MOE_NOT_IMPLEMENTED),  # one workgroup sorts a slice in LDS
+    (dict(dim=9000, k=8193), C.MOE_NOT_IMPLEMENTED),  # long axis: the k winners are sorted in LDS
+    (dict(dim=1 << 31, k=3), C.MOE_NOT_IMPLEMENTED),     # 32-bit indices in LDS
     (dict(k=0), C.MOE_OK),                         # empty output: nothing to launch
     (dict(rows=0), C.MOE_OK),
 ])
@@ -396,3 +397,20 @@ def test_softmax_validation(lib, kw, code):
     for key, val in kw.items():
         setattr(p, key, val)
     assert lib.moe_softmax_launch(ctypes.byref(p), None) == code
+
+
+def test_trace_lines_on_an_error_path(lib, capfd, monkeypatch):
+    # MOE_TRACE_KERNELS is read at creation; a call rejected by validation
+    # (no launch) still prints its begin and end lines, with the status
+    monkeypatch.setenv("MOE_TRACE_KERNELS", "1")
+    st, h = create(lib, "QMoE", k=2, activation_type=4, block_size=128)
+    assert st == C.MOE_OK
+    try:
+        ins = mutate(qmoe_inputs(), 1, dims=[15, 8])
+        arr = (C.MoeTensor * len(ins))(*ins)
+        assert lib.moe_kernel_compute(h, arr, len(ins), FAKE, None, 0, None) == C.MOE_INVALID_ARGUMENT
+    finally:
+        lib.moe_kernel_release(h)
+    err = capfd.readouterr().err
+    assert "MOE_KERNEL_BEGIN QMoE" in err and "MOE_KERNEL_END QMoE" in err
+    assert f"status={C.MOE_INVALID_ARGUMENT} router_probs" in err

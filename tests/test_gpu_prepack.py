@@ -106,6 +106,23 @@ def test_packed_rejects_other_shape(cuda):
     assert ei.value.code == 2
 
 
+def test_packed_rejects_another_tensor_of_the_same_shape(cuda):
+    # a copy of the packed weights (same shape and type, another pointer)
+    # would silently compute with the old packed copy: it is an error; the
+    # packed tensor itself and its packed copy are accepted
+    p = make_problem(replace(C3, hidden=256, inter=512), 16, seed=3, device=cuda, gen="numpy")
+    inputs = p.schema_inputs()
+    op = p.make_op()
+    y0 = op(*inputs).clone()
+    op.prepack_all(*inputs)
+    with pytest.raises(MoeError) as ei:
+        op(*inputs[:5], inputs[5].clone(), *inputs[6:])
+    assert ei.value.code == 2 and "pre-packed" in str(ei.value)
+    y1 = op(*inputs[:5], op._packed[5], *inputs[6:])
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+
+
 def test_packed_needs_an_mfma_path(cuda):
     p = make_problem(replace(C3, hidden=256, inter=512), 8, seed=3, device=cuda, gen="numpy")
     inputs = p.schema_inputs()
