@@ -3,17 +3,26 @@
 
 A step is one QMoE layer invocation (router + dispatch + fc1/fc3 + activation
 + fc2 + finalize) over one batch of synthetic tokens whose inputs and weights
-are already resident in HBM.  The headline workload is BASELINE.json's
-QMoE int8 per-output-channel (fp16 scales), Mixtral shape
+are already resident in HBM.  The headline workload is the configuration the
+decode target is quoted on: QMoE int4 block-128 (fp16 scales), Mixtral shape
 (H=4096, I=14336, E=8, top-2, SwiGLU fc1/fc3 unfused), fp16 activations, at
 16 tokens (decode).  The other configurations are reported under "extra".
+
+Decode workloads whose routed weights are smaller than twice the 256 MB
+Infinity Cache (e.g. 2 Mixtral int4 experts at T=1) rotate through enough
+copies of the expert weights (at least 4, together at least 1 GiB) that no
+step can find the previous step's weights in a cache: every step reads its
+weights from HBM.
 
 Roofline: the dominant kernel's algorithmic bytes (decode) or FLOPs (prefill)
 per launch divided by its mean duration, timed with HIP events recorded by the
 library on the stream the kernels run on (moe_kernel_stage_times).
 
 cpu_baseline: the oracle (C restatement, OpenMP) on the same inputs on the
-host cores of this box.  It is a reported baseline, not the target.
+host cores this process may use (its affinity mask, or OMP_NUM_THREADS where
+that is smaller: the CPU share a GPU box allots).  It is a reported
+baseline, not the target.  A second line times the prefill layer (C3 T=4096)
+on a sample of its tokens.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
 """
@@ -35,9 +44,11 @@ PEAK_HBM_GBS = 8000.0   # MI355X HBM3E
 PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16/bf16
 
 METRIC = "QMoE layer tokens/s; HBM GB/s at decode, MFMA TFLOP/s at prefill, % roofline"
-HEADLINE = ("c2_qmoe_int8_mixtral", 16)
-EXTRA = [("c2_qmoe_int8_mixtral", 1), ("c2_qmoe_int8_mixtral", 4096),
-         ("c3_qmoe_int4_mixtral", 1), ("c3_qmoe_int4_mixtral", 16), ("c3_qmoe_int4_mixtral", 4096),
+HEADLINE = ("c3_qmoe_int4_mixtral", 16)
+CPU_PREFILL = ("c3_qmoe_int4_mixtral", 4096, 512)  # workload, tokens, tokens sampled on the CPU
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+EXTRA = [("c2_qmoe_int8_mixtral", 1), ("c2_qmoe_int8_mixtral", 16), ("c2_qmoe_int8_mixtral", 4096),
+         ("c3_qmoe_int4_mixtral", 1), ("c3_qmoe_int4_mixtral", 4096),
          ("c4_qmoe_int4_gptoss", 1), ("c4_qmoe_int4_gptoss", 64), ("c4_qmoe_int4_gptoss", 8192),
          ("c5_moe_f16_qwen3", 8192), ("c1_moe_f32", 64)]
 
@@ -88,6 +99,20 @@ def measured_traffic(key: str):
     return ent["bytes"] if ent else None
 
 
+WEIGHT_NAMES = ("fc1_experts_weights", "fc1_scales", "fc1_experts_bias", "fc2_experts_weights", "fc2_scales",
+                "fc2_experts_bias", "fc3_experts_weights", "fc3_scales", "fc3_experts_bias")
+
+
+def weight_copies(routed_bytes: int) -> int:
+    """Copies of the expert weights a decode step rotates through: 1 when the
+    routed weights are at least twice the Infinity Cache, else enough copies
+    (at least 4, together at least 1 GiB) that a step never finds its weights
+    still cached from an earlier step."""
+    if routed_bytes >= 2 * MALL_BYTES:
+        return 1
+    return max(4, -(-(4 * MALL_BYTES) // max(routed_bytes, 1)))
+
+
 def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=False, prepack=True):
     import torch
 
@@ -95,41 +120,66 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
 
     cfg = CONFIGS[name]
     prob = make_problem(cfg, T, seed=1234, device=dev)
-    op = prob.make_op()
     inputs = prob.schema_inputs()
-    # session set-up: QMoE expert weights pre-packed once (not timed), as a
-    # plugin EP's PrePack does for constant initializers
-    packed = op.prepack_all(*inputs) if prepack else []
+    names = prob.input_names[:len(inputs)]
+    ws = out = None
+
+    def build(ins):
+        """One op over `ins`; session set-up: QMoE expert weights pre-packed
+        once (not timed), as a plugin EP's PrePack does for constant
+        initializers.  Returns (op, its call, packed input indices)."""
+        nonlocal ws, out
+        op = prob.make_op()
+        packed = op.prepack_all(*ins) if prepack else []
+        ins = [None if i in packed else t for i, t in enumerate(ins)]
+        if ws is None:
+            ws = torch.empty((op.workspace_size(*ins),), dtype=torch.uint8, device=dev)
+            out = torch.empty_like(inputs[0])
+        return op, op.bind(*ins, out=out, workspace=ws), packed
+
+    op, call, packed = build(inputs)
+    call()
     torch.cuda.synchronize()
-    ws = torch.empty((op.workspace_size(*inputs),), dtype=torch.uint8, device=dev)
-    out = torch.empty_like(inputs[0])
-    call = op.bind(*inputs, out=out, workspace=ws)
-    for _ in range(warmup):
-        call()
+    # routing of this workload: experts actually hit
+    lay = op.workspace_layout(*[None if i in packed else t for i, t in enumerate(inputs)])
+    offs = ws[lay["offsets"]:lay["offsets"] + 4 * (cfg.experts + 1)].view(torch.int32).cpu()
+    hit = int((offs[1:] - offs[:-1] > 0).sum())
+    cost = kernel_cost(cfg, T, hit)
+    decode_sized = T <= 64
+    ncopy = weight_copies(hit * (expert_bytes(cfg, "fc1") + expert_bytes(cfg, "fc2"))) if decode_sized else 1
+    ops, calls = [op], [call]
+    for _ in range(ncopy - 1):
+        # the same weights at other addresses (the row-major copy is dropped
+        # once packed)
+        ins = [t.clone() if (t is not None and n in WEIGHT_NAMES) else t for n, t in zip(names, inputs)]
+        o, c, _ = build(ins)
+        ops.append(o)
+        calls.append(c)
+        del ins
+    torch.cuda.synchronize()
+    for i in range(warmup):
+        calls[i % ncopy]()
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record()
-    for _ in range(steps):
-        call()
+    for i in range(steps):
+        calls[i % ncopy]()
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = max(start.elapsed_time(stop), wall * 1e3) / steps
-    # routing of this workload: experts actually hit
-    lay = op.workspace_layout(*inputs)
-    offs = ws[lay["offsets"]:lay["offsets"] + 4 * (cfg.experts + 1)].view(torch.int32).cpu()
-    hit = int((offs[1:] - offs[:-1] > 0).sum())
     # per-stage timing pass (events recorded by the library on the kernels' stream)
-    op.set_profiling(True)
+    for o in ops:
+        o.set_profiling(True)
     stages = []
-    for _ in range(steps):
-        call()
-        stages.append(op.stage_times())
-    op.set_profiling(False)
+    for i in range(steps):
+        calls[i % ncopy]()
+        stages.append(ops[i % ncopy].stage_times())
+    for o in ops:
+        o.set_profiling(False)
     path = stages[-1]["path"]
     st = {k: statistics.mean(s[k] for s in stages) for k in ("route_dispatch", "fc1", "fc2", "finalize")}
-    cost = kernel_cost(cfg, T, hit)
     decode = path != "prefill"
     traffic = measured_traffic(f"{name}:{T}")
     if decode:
@@ -142,16 +192,18 @@ def run_workload(name: str, T: int, steps: int, warmup: int, dev, keep_problem=F
                     frac=round(fc1_ach / PEAK_MFMA_TFLOPS, 4), traffic=traffic)
     layer_s = ms_per_step * 1e-3
     res = dict(workload=name, tokens=T, path=path, prepacked=packed, ms_per_step=round(ms_per_step, 4),
-               tokens_per_s=round(T / layer_s, 1), experts_hit=hit,
+               tokens_per_s=round(T / layer_s, 1), experts_hit=hit, weight_copies=ncopy,
                layer_hbm_gbs=round(cost["layer_bytes"] / layer_s / 1e9, 1),
                layer_tflops=round(cost["layer_flops"] / layer_s / 1e12, 2),
                stages_ms={k: round(v, 4) for k, v in st.items()},
                fc2=dict(achieved_gbs=round(cost["fc2_bytes"] / (st["fc2"] * 1e-3) / 1e9, 1),
                         achieved_tflops=round(cost["fc2_flops"] / (st["fc2"] * 1e-3) / 1e12, 2)),
                roofline=roof, algorithmic=dict(fc1_bytes=cost["fc1_bytes"], fc1_flops=cost["fc1_flops"]))
+    del ops, calls, op, call, ws, out
     if keep_problem:
+        torch.cuda.empty_cache()
         return res, prob
-    del op, ws, out, call, prob, inputs
+    del prob, inputs
     torch.cuda.empty_cache()
     return res, None
 
@@ -210,27 +262,51 @@ def run_op(spec: str, steps: int, warmup: int, dev) -> dict:
                               frac=round(gbs / PEAK_HBM_GBS, 4)))
 
 
-def cpu_baseline(prob, budget_s: float = 12.0):
-    """Times the oracle on the headline workload on this host's cores."""
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(prob, budget_s: float = 12.0, sample_tokens=None):
+    """Times the oracle on a workload on this host's cores: every core of
+    the affinity mask, or OMP_NUM_THREADS where that is smaller (the CPU
+    share a GPU box allots).  sample_tokens: compute the expert FFN for that
+    many seeded token samples only (routing for every token); tokens/s is
+    then sample_tokens / time."""
     import numpy as np
 
     from onnxruntime_musa_amd.workloads import to_host
     from oracle import oracle
 
-    cores = int(os.environ.get("OMP_NUM_THREADS") or 0) or len(os.sched_getaffinity(0))
-    cores = max(1, min(cores, 16, len(os.sched_getaffinity(0))))
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS") or affinity))
     host = {n: to_host(t) for n, t in prob.inputs.items()}
-    oracle.forward_problem(prob.cfg, host, threads=cores)  # warm-up
+    T = prob.tokens
+    mask, counted = None, T
+    if sample_tokens is not None and sample_tokens < T:
+        rows = np.random.default_rng(0).choice(T, size=sample_tokens, replace=False)
+        mask = np.zeros(T, np.uint8)
+        mask[rows] = 1
+        counted = sample_tokens
+    oracle.forward_problem(prob.cfg, host, token_mask=mask, threads=cores)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
     while len(times) < 5 and (not times or time.perf_counter() < t_end):
         t0 = time.perf_counter()
-        oracle.forward_problem(prob.cfg, host, threads=cores)
+        oracle.forward_problem(prob.cfg, host, token_mask=mask, threads=cores)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    return dict(value=round(prob.tokens / med, 2), unit="tokens/s", cores=cores, kind="port",
-                sample=f"{prob.cfg.name} full layer, {prob.tokens} tokens, {len(times)} timed runs "
-                       f"(median {med * 1e3:.1f} ms), OpenMP fp32 restatement")
+    what = f"{T} tokens" if mask is None else f"{counted} of {T} tokens (seeded sample; routing for all)"
+    return dict(value=round(counted / med, 2), unit="tokens/s", cores=cores, kind="port",
+                sample=f"{prob.cfg.name} layer, {what}, {len(times)} timed runs (median {med * 1e3:.1f} ms), "
+                       f"OpenMP fp32 restatement on {cores} threads of {affinity} in the affinity mask, "
+                       f"{cpu_model()}")
 
 
 def main():
@@ -284,10 +360,18 @@ def main():
     del prob
     torch.cuda.empty_cache()
     extra = []
+    cpu_prefill = None
     if not args.no_extra and not args.workload:
         for wname, wT in EXTRA:
-            r, _ = run_workload(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev,
-                                prepack=not args.no_prepack)
+            keep = not args.no_cpu and (wname, wT) == CPU_PREFILL[:2]
+            r, wprob = run_workload(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev,
+                                    keep_problem=keep, prepack=not args.no_prepack)
+            if wprob is not None:
+                cpu_prefill = cpu_baseline(wprob, sample_tokens=CPU_PREFILL[2])
+                cpu_prefill["gpu_tokens_per_s"] = r["tokens_per_s"]
+                print(f"[bench] cpu baseline (prefill): {cpu_prefill}", file=sys.stderr, flush=True)
+                del wprob
+                torch.cuda.empty_cache()
             extra.append(r)
             print(f"[bench] {wname} T={wT}: {r['tokens_per_s']} tok/s, {r['ms_per_step']} ms, path={r['path']}, "
                   f"fc1 {r['roofline']['achieved']} {r['roofline']['unit']} ({r['roofline']['frac']:.1%})",
@@ -312,9 +396,11 @@ def main():
                    "weights": (f"int{cfg.bits} " + (f"block {cfg.block_size}" if cfg.block_size else "per-channel")
                                + f", {cfg.scale_dtype} scales") if cfg.bits else cfg.dtype,
                    "path": head["path"], "experts_hit": head["experts_hit"],
+                   "weight_copies": head["weight_copies"],
                    "prepacked_inputs": head["prepacked"]},
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
+        "cpu_baseline_prefill": cpu_prefill,
         "stages_ms": head["stages_ms"],
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "extra": extra,

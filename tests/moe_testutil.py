@@ -29,6 +29,15 @@ def compare_outputs(got: np.ndarray, exp: np.ndarray, dtype: str, what: str, row
     return float(np.max(np.abs(g - e))) if g.size else 0.0
 
 
+def tolerance_margin(got: np.ndarray, exp: np.ndarray, dtype: str) -> float:
+    """max over elements of |got - exp| / (atol + rtol |exp|): the share of
+    the tolerance the worst element uses (the test fails above 1)."""
+    g = oracle.to_f32(got, dtype).astype(np.float64)
+    e = oracle.to_f32(exp, dtype).astype(np.float64)
+    rtol, atol = TOL[dtype]
+    return float(np.max(np.abs(g - e) / (atol + rtol * np.abs(e)))) if g.size else 0.0
+
+
 def run_op(problem: Problem, path: str = "auto", with_workspace: bool = False, prepack: bool = False):
     op = problem.make_op(expert_path=path)
     inputs = problem.schema_inputs()
@@ -57,10 +66,12 @@ def run_op(problem: Problem, path: str = "auto", with_workspace: bool = False, p
     return y, routing
 
 
-def check_problem(problem: Problem, path: str = "auto", sample_tokens=None, seed=0, threads=0, prepack=False):
+def check_problem(problem: Problem, path: str = "auto", sample_tokens=None, seed=0, threads=0, prepack=False,
+                  report=False):
     """Runs the HIP op and the oracle on the same inputs and compares.
     sample_tokens: compute the oracle's expert FFN for this many sampled tokens
-    only (routing is still checked for every token)."""
+    only (routing is still checked for every token).  report: print the
+    largest error and the share of the tolerance it uses."""
     y, routing = run_op(problem, path, with_workspace=True, prepack=prepack)
     host = {n: to_host(t) for n, t in problem.inputs.items()}
     T = problem.tokens
@@ -79,5 +90,12 @@ def check_problem(problem: Problem, path: str = "auto", sample_tokens=None, seed
         np.testing.assert_array_equal(routing["inv_perm"][routing["perm"]], np.arange(T * problem.cfg.k),
                                       err_msg="inverse permutation")
     np.testing.assert_allclose(routing["topk_w"], ref["topk_w"], rtol=2e-6, atol=1e-7, err_msg="routing weights")
-    return compare_outputs(to_host(y), ref["out"], problem.cfg.dtype, f"{problem.cfg.name} T={T} path={path}",
-                           rows=rows)
+    what = f"{problem.cfg.name} T={T} path={path}"
+    got = to_host(y)
+    if report:
+        g, e = (got, ref["out"]) if rows is None else (got[rows], ref["out"][rows])
+        err = float(np.max(np.abs(oracle.to_f32(g, problem.cfg.dtype) - oracle.to_f32(e, problem.cfg.dtype))))
+        print(f"[parity] {what}: max|err| {err:.3e}, worst element at "
+              f"{tolerance_margin(g, e, problem.cfg.dtype):.3f} of the tolerance "
+              f"({'all' if rows is None else len(rows)} tokens compared)", flush=True)
+    return compare_outputs(got, ref["out"], problem.cfg.dtype, what, rows=rows)
