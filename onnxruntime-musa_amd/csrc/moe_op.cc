@@ -286,19 +286,19 @@ moe_status with_packed(const moe_kernel* kr, const moe_tensor* inputs, int32_t n
   for (int32_t i = 0; i < n && i < 11; ++i) {
     const auto& pk = kr->packed[i];
     if (!pk.data) continue;
-    if (inputs[i].data) {
+    if (inputs[i].data && inputs[i].data != pk.data) {
       bool same = inputs[i].elem_type == pk.src.elem_type && inputs[i].rank == pk.src.rank;
       for (int d = 0; same && d < pk.src.rank; ++d) same = inputs[i].dims[d] == pk.src.dims[d];
       if (!same)
         return fail(MOE_INVALID_ARGUMENT, "input " + std::to_string(i) + " " + dims_str(inputs[i]) +
                                               " differs from the pre-packed weights " + dims_str(pk.src));
-      if (inputs[i].data != pk.src.data && inputs[i].data != pk.data)
+      if (inputs[i].data != pk.src.data)
         return fail(MOE_INVALID_ARGUMENT, "input " + std::to_string(i) +
                                               " is not the tensor that was pre-packed (another data pointer); "
                                               "pass that tensor, its packed copy or NULL");
-    } else {
-      local[i] = pk.src;
     }
+    // the packed copy (whatever its descriptor) or NULL: the packed tensor's shape
+    local[i] = pk.src;
     local[i].data = pk.data;
   }
   return MOE_OK;
