@@ -154,6 +154,25 @@ MOE_API moe_status moe_kernel_compute(const moe_kernel *kernel, const moe_tensor
 
 MOE_API void moe_kernel_release(moe_kernel *kernel);
 
+/* Runs the op like moe_kernel_compute, allocating nothing: the workspace is
+ * a static device array of the library, MOE_NOALLOC_SCRATCH_BYTES (64 MiB)
+ * on each GPU it runs on, held from the library's first use of that GPU
+ * until the process ends.  No counterpart in the reference: this is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops and harnesses that forbid hipMalloc).  It calls no
+ * hipMalloc/hipFree and does not synchronise.  A problem whose workspace
+ * (moe_kernel_workspace_size) exceeds the array returns
+ * MOE_INVALID_ARGUMENT; decode batches fit (Mixtral-shaped QMoE at 64
+ * tokens needs 19.5 MiB, gpt-oss-shaped at 512 tokens 34 MiB), large
+ * prefill batches do not.  Every call on
+ * one GPU uses the same array, so calls that overlap on one GPU (several
+ * streams or threads) race: serialise them on one stream, or give each its
+ * own workspace through moe_kernel_compute.  No part of the array needs
+ * clearing between calls (each call writes every byte it reads). */
+#define MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+MOE_API moe_status moe_kernel_compute_noalloc(const moe_kernel *kernel, const moe_tensor *inputs,
+                                              int32_t num_inputs, void *output, void *stream);
+
 /* Byte offsets, inside a caller-provided workspace, of the routing results a
  * moe_kernel_compute call leaves there (int32 topk_ids[T*k], float
  * topk_w[T*k], int32 offsets[E+1], int32 perm[T*k], int32 inv_perm[T*k]) and

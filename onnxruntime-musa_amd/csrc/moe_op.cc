@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -702,6 +703,43 @@ moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int3
 
 }  // namespace
 
+// Scratch of moe_kernel_compute_noalloc: the workspace of callers that
+// cannot allocate device memory.  The host-side name is only a stand-in for
+// the array: host code uses the device address that scratch_address() looks
+// up once per device (each GPU holds its own copy, from the library's first
+// use on it until the process ends).
+static __device__ __align__(256) uint8_t scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kScratchDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array.
+moe_status scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(MOE_EP_FAIL, "device " + std::to_string(dev) + " is beyond the scratch table");
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      if (!p) return fail(MOE_EP_FAIL, "hipGetSymbolAddress(scratch) returned NULL");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MOE_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
@@ -720,6 +758,27 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     std::fflush(stderr);
   }
   return st;
+}
+
+moe_status moe_kernel_compute_noalloc(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
+                                      void* stream) {
+  try {
+    if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+    size_t need = 0;
+    moe_status st = moe_kernel_workspace_size(kernel, inputs, n, &need);
+    if (st != MOE_OK) return st;
+    if (need > MOE_NOALLOC_SCRATCH_BYTES)
+      return fail(MOE_INVALID_ARGUMENT, "moe_kernel_compute_noalloc: this call needs " + std::to_string(need) +
+                                            " bytes of workspace, more than the library's scratch (" +
+                                            std::to_string(static_cast<size_t>(MOE_NOALLOC_SCRATCH_BYTES)) +
+                                            " bytes); pass a workspace to moe_kernel_compute instead");
+    void* ws = nullptr;
+    st = scratch_address(&ws);
+    if (st != MOE_OK) return st;
+    return moe_kernel_compute(kernel, inputs, n, output, ws, MOE_NOALLOC_SCRATCH_BYTES, stream);
+  } catch (const std::exception& e) {
+    return fail(MOE_FAIL, e.what());
+  }
 }
 
 void moe_kernel_release(moe_kernel* kernel) { delete kernel; }

@@ -115,6 +115,8 @@ EXPORTS = [
     ("moe_kernel_compute", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("moe_kernel_release", None, [ctypes.c_void_p]),
+    ("moe_kernel_compute_noalloc", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
+                                                  ctypes.c_void_p, ctypes.c_void_p]),
     ("moe_kernel_workspace_layout", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                                    ctypes.POINTER(MoeWorkspaceLayout)]),
     ("moe_kernel_set_expert_path", ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),

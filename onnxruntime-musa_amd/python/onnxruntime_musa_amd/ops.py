@@ -181,6 +181,19 @@ class _MoEOp:
                                            ws_bytes, ctypes.c_void_p(s.cuda_stream)))
         return out
 
+    def compute_noalloc(self, *inputs, out: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """The op on the library's static scratch (moe_kernel_compute_noalloc):
+        no device allocation, for callers that cannot allocate.  `out` is
+        given by the caller.  Calls that overlap on one GPU race."""
+        arr, n = self._descs(inputs)
+        x = inputs[0]
+        if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("out must match the input's shape and dtype")
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        check(self._lib.moe_kernel_compute_noalloc(self._h, arr, n, out.data_ptr() if out.numel() else None,
+                                                   ctypes.c_void_p(s.cuda_stream)))
+        return out
+
     def bind(self, *inputs, out: torch.Tensor, workspace: torch.Tensor,
              stream: Optional[torch.cuda.Stream] = None):
         """Pre-builds the C arguments for repeated calls on fixed buffers (a
