@@ -105,15 +105,16 @@ template <typename ST, int NSC>
 struct ScaleRaw {
   static constexpr int kBytes = NSC * static_cast<int>(sizeof(typename ST::storage));
   using type = std::conditional_t<(kBytes > 8), u32x4_t, std::conditional_t<(kBytes > 4), u32x2_t, uint32_t>>;
+  template <int AUX>
   __device__ static __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     if constexpr (kBytes == 2) {
-      return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0));
+      return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, AUX));
     } else if constexpr (kBytes == 4) {
-      return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, AUX);
     } else if constexpr (kBytes == 8) {
-      return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0));
+      return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, AUX));
     } else {
-      return bload16(r, off);
+      return bload16_aux<AUX>(r, off);
     }
   }
   __device__ static __forceinline__ float elem(type v, int i) {
@@ -185,9 +186,12 @@ inline size_t stream_lds_bytes(int ksc, int ngroups, int nw, int route_ints) {
 // NSC: folded scales (block 16/32/64): elements per lane and chunk (2 for
 // block 16); block scales: 4 = one load brings the scales of 4 chunks
 // (block 128, K a multiple of 512), 1 = one load per chunk.
-template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATED>
+// STREAM_NT: the weights are tile-major (pre-packed), streamed with the
+// non-temporal cache policy.
+template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATED, bool STREAM_NT>
 __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_kernel(StreamStage ss) {
   using G = SGeo<WF, GATED>;
+  constexpr int kAux = STREAM_NT ? kStreamAux : 0;
   constexpr int NW = G::NW, NT = NW * 64, WT = G::WT, FT = G::FT, PD = G::PD, LB = G::kLaneBytes;
   constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan);
   constexpr bool kSplit = kBiased && WF == kInt4 && AT::kId == 10;
@@ -320,7 +324,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // are one contiguous block, lane l's 16 bytes at 16 l (vector v of int8
   // one 1 KB block further), so that each load instruction reads 1 KB in
   // one run.  Row-major: row col, bytes [LB g, LB g + LB) of the chunk.
-  const bool tiled = p.tiled != 0;
+  const bool tiled = STREAM_NT || p.tiled != 0;
   const uint32_t cstride = tiled ? 64 * LB : 4 * LB;  // weight bytes per chunk
   const int vdelta = tiled ? 1024 - 16 : 0;           // extra offset of vector v, per v
   int fo[WT], rowb[WT];
@@ -390,7 +394,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         tile_offs(tl, woff, soff);
 #pragma unroll
         for (int u = 0; u < WT; ++u)
-          tsr[u] = bload16(GATED && u >= FT ? ss_l : ss_g, soff[u] + static_cast<uint32_t>(cs0) * 2 + 16 * g);
+          tsr[u] = bload16_aux<kAux>(GATED && u >= FT ? ss_l : ss_g, soff[u] + static_cast<uint32_t>(cs0) * 2 + 16 * g);
       }
     };
     // vector memory loads that fetching one block issues
@@ -410,14 +414,14 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         for (int v = 0; v < G::kVecs; ++v)
           d.w[u][v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                                       GATED && u >= FT ? rs_l : rs_g, static_cast<int>(o + 16 * v),
-                                                      v * vdelta, 0));
+                                                      v * vdelta, kAux));
         if constexpr (kRingScales && !kTileScales) {
           const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (SM == kScaleFold ? 32 * g : 0);
           // a block scale multiplies the whole chunk's sum (every lane group
           // of the MFMA output), so only a chunk past K reads none
           const uint32_t so = (soff[u] + (kk >> bshift) * kEs) | (SM == kScaleFold ? oob : (cg < nchunks ? 0u : kOob));
           // grouped: the first chunk of each group of 4 loads all 4 scales
-          if (!kGroupScales || (cl & 3) == 0) d.sc[u] = SR::load(GATED && u >= FT ? ss_l : ss_g, so);
+          if (!kGroupScales || (cl & 3) == 0) d.sc[u] = SR::template load<kAux>(GATED && u >= FT ? ss_l : ss_g, so);
         }
       }
     };
@@ -764,7 +768,8 @@ int stream_grid(int nw);
 template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATED>
 hipError_t launch_stream(const StreamStage& ss, hipStream_t stream) {
   using G = SGeo<WF, GATED>;
-  auto kern = gemv_stream_kernel<AT, WF, SM, ST, NSC, FC1, GATED>;
+  auto kern = ss.s.tiled ? gemv_stream_kernel<AT, WF, SM, ST, NSC, FC1, GATED, true>
+                         : gemv_stream_kernel<AT, WF, SM, ST, NSC, FC1, GATED, false>;
   const size_t lds = stream_lds_bytes(ss.ksc, ss.ngroups, G::NW, ss.route_ints);  // <= 157 KB
   hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(stream_grid(G::NW))), dim3(G::NW * 64), lds, stream, ss);
   return hipGetLastError();
