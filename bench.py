@@ -262,6 +262,63 @@ def run_op(spec: str, steps: int, warmup: int, dev) -> dict:
                               frac=round(gbs / PEAK_HBM_GBS, 4)))
 
 
+ROUTER_FUSION = [("c3_qmoe_int4_mixtral", 16), ("c3_qmoe_int4_mixtral", 4096), ("c4_qmoe_int4_gptoss", 16)]
+
+
+def run_router_fusion(name: str, T: int, steps: int, warmup: int, dev) -> dict:
+    """The router GEMM fused into the op (moe_kernel_compute_fused_router)
+    against the unfused pair it replaces: the graph's gate MatMul (torch's,
+    hipBLASLt) writing the logits, then the op reading them.  Random
+    [E, H] gate weights of the activation type."""
+    import torch
+
+    from onnxruntime_musa_amd.workloads import CONFIGS, make_problem
+
+    cfg = CONFIGS[name]
+    prob = make_problem(cfg, T, seed=1234, device=dev)
+    x = prob.inputs["input"]
+    g = torch.Generator(device=dev)
+    g.manual_seed(77)
+    wg = (torch.randn((cfg.experts, cfg.hidden), generator=g, device=dev) / cfg.hidden ** 0.5).to(x.dtype)
+    wt = wg.t().contiguous()  # the MatMul's [H, E] operand
+    op = prob.make_op()
+    ins = prob.schema_inputs()
+    packed = op.prepack_all(*ins)
+    ins = [None if i in packed else t for i, t in enumerate(ins)]
+    ws = torch.empty((op.workspace_size(*ins),), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(x)
+    logits = torch.empty_like(prob.inputs["router_probs"])
+    ins_u = list(ins)
+    ins_u[1] = logits
+    call_u = op.bind(*ins_u, out=out, workspace=ws)
+    ins_f = list(ins)
+    ins_f[1] = None
+    call_f = op.bind_fused_router(*ins_f, router_weight=wg, out=out, workspace=ws)
+
+    def unfused():
+        torch.matmul(x, wt, out=logits)
+        call_u()
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+
+    tu, tf = timed(unfused), timed(call_f)
+    res = dict(workload=name, tokens=T, unfused_ms=round(tu, 4), fused_ms=round(tf, 4),
+               saved_us=round((tu - tf) * 1e3, 1))
+    del op, ws, out, prob, ins, ins_u, ins_f, call_u, call_f
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_model() -> str:
     """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
     try:
@@ -376,6 +433,13 @@ def main():
             print(f"[bench] {wname} T={wT}: {r['tokens_per_s']} tok/s, {r['ms_per_step']} ms, path={r['path']}, "
                   f"fc1 {r['roofline']['achieved']} {r['roofline']['unit']} ({r['roofline']['frac']:.1%})",
                   file=sys.stderr, flush=True)
+    fusion = []
+    if not args.no_extra and not args.workload:
+        for wname, wT in ROUTER_FUSION:
+            r = run_router_fusion(wname, wT, max(10, args.steps // 2), max(3, args.warmup // 2), dev)
+            fusion.append(r)
+            print(f"[bench] router GEMM fusion {wname} T={wT}: unfused {r['unfused_ms']} ms, fused {r['fused_ms']} ms",
+                  file=sys.stderr, flush=True)
     from onnxruntime_musa_amd.workloads import CONFIGS
     cfg = CONFIGS[name]
     line = {
@@ -404,6 +468,7 @@ def main():
         "stages_ms": head["stages_ms"],
         "layer_hbm_gbs": head["layer_hbm_gbs"],
         "extra": extra,
+        "router_gemm_fusion": fusion,
     }
     print(json.dumps(line), flush=True)
 

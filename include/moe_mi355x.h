@@ -154,6 +154,28 @@ MOE_API moe_status moe_kernel_compute(const moe_kernel *kernel, const moe_tensor
 
 MOE_API void moe_kernel_release(moe_kernel *kernel);
 
+/* Router-GEMM fusion: the op with its router logits computed in the routing
+ * kernels instead of taken as an input.  router_probs (inputs[1]) may be
+ * absent (data == NULL; the other inputs as for moe_kernel_compute):
+ *   logits[t, e] = sum_h input[t, h] * router_weight[e, h] (+ router_bias[e])
+ * with fp32 accumulation, rounded once to the input's type (as the graph's
+ * separate MatMul would store them), then routed as router_probs would be.
+ * router_weight is [num_experts, hidden_size] of the input's type: the
+ * transposed B operand of the MatMul(x, W[hidden, experts]) that feeds the
+ * MoE node (a plugin EP transposes that initializer once, at set-up);
+ * router_bias is [num_experts] or NULL.  The routing kernels compute each
+ * token's logits and route it in the same launch.  This replaces the
+ * MatMul -> MoE node pair that the reference's fusion machinery matches and
+ * compiles into one node (musa/ep/src/fusion/fusion_matcher.h:26-34,
+ * musa/ep/src/fusion/fusion_node_compute.cc:201-300).  The workspace is the
+ * same as moe_kernel_compute's (moe_kernel_workspace_size with router_probs
+ * described as [T, num_experts]; only shapes are read); the logits it
+ * leaves there are at moe_workspace_layout.logits. */
+MOE_API moe_status moe_kernel_compute_fused_router(const moe_kernel *kernel, const moe_tensor *inputs,
+                                                   int32_t num_inputs, const moe_tensor *router_weight,
+                                                   const moe_tensor *router_bias, void *output,
+                                                   void *workspace, size_t workspace_bytes, void *stream);
+
 /* Runs the op like moe_kernel_compute, allocating nothing: the workspace is
  * a static device array of the library, MOE_NOALLOC_SCRATCH_BYTES (64 MiB)
  * on each GPU it runs on, held from the library's first use of that GPU
@@ -184,6 +206,7 @@ MOE_API moe_status moe_kernel_compute_noalloc(const moe_kernel *kernel, const mo
 typedef struct moe_workspace_layout {
   size_t topk_ids, topk_w, offsets, perm, inv_perm, total;
   size_t act, y2, y2_planes_max;
+  size_t logits; /* [T, E] of the input's type: the fused router's logits */
 } moe_workspace_layout;
 MOE_API moe_status moe_kernel_workspace_layout(const moe_kernel *kernel, const moe_tensor *inputs,
                                        int32_t num_inputs, moe_workspace_layout *out);

@@ -36,9 +36,23 @@ struct RouteArgs {
   moe_route_params p;
   int32_t* tile_offsets;  // optional [E+1]: prefix of ceil(count_e / tile_m)
   int32_t tile_m;
+  // Router GEMM fused into the routing kernels (gate_w non-null): the
+  // logits [T, E] = x [T, H] * gate_w [E, H]^T (+ gate_b [E]) are computed
+  // with fp32 accumulation, rounded to the logits type and written to
+  // p.logits (a workspace buffer) by the workgroup that routes those tokens.
+  const void* gate_x;
+  const void* gate_w;
+  const void* gate_b;
+  int64_t hidden;
 };
+// Largest T * E * H routed by the single-workgroup router with the router
+// GEMM fused (larger products take the multi-workgroup router).
+constexpr int64_t kGateSmallMacs = int64_t{1} << 22;
 
 size_t route_scratch_bytes(int64_t T, int64_t E, int64_t k);
+// Scratch of the routing kernels with the router GEMM fused (every T > 0 may
+// take the multi-workgroup router).
+size_t route_scratch_bytes_gate(int64_t T, int64_t E);
 hipError_t launch_route_dispatch(const RouteArgs& a, hipStream_t stream);
 
 struct ExpertArgs {

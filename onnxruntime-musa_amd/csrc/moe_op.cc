@@ -69,7 +69,7 @@ struct Problem {
 
 // Workspace sections, byte offsets from the workspace base.
 struct Layout {
-  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, act, y2, total;
+  size_t topk_ids, topk_w, offsets, tile_offsets, perm, inv_perm, route_scratch, logits, act, y2, total;
   int32_t y2_planes;
   size_t route_scratch_bytes;
   moe::DecodePlan decode;
@@ -90,8 +90,11 @@ Layout plan_layout(const Problem& p) {
   l.tile_offsets = take(static_cast<size_t>(p.E + 1) * 4);
   l.perm = take(rows * 4);
   l.inv_perm = take(rows * 4);
-  l.route_scratch_bytes = moe::route_scratch_bytes(p.T, p.E, p.k);
+  // routing scratch for either router (logits given, or the router GEMM
+  // fused), and the logits the fused router writes
+  l.route_scratch_bytes = std::max(moe::route_scratch_bytes(p.T, p.E, p.k), moe::route_scratch_bytes_gate(p.T, p.E));
   l.route_scratch = take(l.route_scratch_bytes);
+  l.logits = take(static_cast<size_t>(p.T * p.E) * elem_size(p.act_type));
   l.act = take(rows * static_cast<size_t>(p.I) * elem_size(p.act_type));
   l.decode = moe::plan_decode(p.T, p.H, p.I, p.E, p.k, p.wfmt, p.gate_mode);
   l.y2_planes = std::max<int32_t>({1, l.decode.y2_planes_max,
@@ -558,6 +561,7 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
     out->act = l.act;
     out->y2 = l.y2;
     out->y2_planes_max = static_cast<size_t>(l.y2_planes);
+    out->logits = l.logits;
     return MOE_OK;
   } catch (const std::exception& e) {
     return fail(MOE_FAIL, e.what());
@@ -568,13 +572,44 @@ moe_status moe_kernel_workspace_layout(const moe_kernel* kernel, const moe_tenso
 
 namespace {
 
+// The router GEMM's operands: gate_w [E, H] of the input's type (the
+// transposed B operand of the graph's MatMul(x, W[H, E])), gate_b [E] or
+// NULL.  Fills the router_probs descriptor of `local` (shape [T, E]; its data
+// is the workspace's logits buffer, set once the workspace is known).
+moe_status gate_router_input(const moe_tensor* gate_w, const moe_tensor* gate_b, moe_tensor* local, int32_t n) {
+  if (!gate_w || !gate_w->data) return fail(MOE_INVALID_ARGUMENT, "router_weight is required");
+  if (n < 2) return fail(MOE_INVALID_ARGUMENT, "too few inputs");
+  const moe_tensor& x = local[0];
+  if (!x.data || (x.rank != 2 && x.rank != 3)) return fail(MOE_INVALID_ARGUMENT, "input must be 2D or 3D");
+  const int64_t H = x.dims[x.rank - 1], T = x.dims[0] * (x.rank == 3 ? x.dims[1] : 1);
+  if (gate_w->rank != 2 || gate_w->dims[1] != H || gate_w->dims[0] <= 0)
+    return fail(MOE_INVALID_ARGUMENT, "router_weight must be [num_experts, hidden_size], got " + dims_str(*gate_w));
+  if (gate_w->elem_type != x.elem_type) return fail(MOE_INVALID_ARGUMENT, "router_weight must have the input's type");
+  const int64_t es = elem_size(x.elem_type);
+  if (T * H * es >= (int64_t{1} << 31) || gate_w->dims[0] * H * es >= (int64_t{1} << 31))
+    return fail(MOE_NOT_IMPLEMENTED, "the fused router reads input and router_weight with 32-bit offsets (< 2 GiB each)");
+  if (gate_b && gate_b->data &&
+      (gate_b->rank != 1 || gate_b->dims[0] != gate_w->dims[0] || gate_b->elem_type != x.elem_type))
+    return fail(MOE_INVALID_ARGUMENT, "router_bias must be [num_experts] of the input's type, got " + dims_str(*gate_b));
+  moe_tensor r{};
+  r.data = gate_w->data;  // placeholder for validation; replaced by the logits buffer
+  r.elem_type = x.elem_type;
+  r.rank = 2;
+  r.dims[0] = T;
+  r.dims[1] = gate_w->dims[0];
+  local[1] = r;
+  return MOE_OK;
+}
+
 moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n, void* output,
-                        void* workspace, size_t workspace_bytes, void* stream_ptr) {
+                        void* workspace, size_t workspace_bytes, void* stream_ptr,
+                        const moe_tensor* gate_w = nullptr, const moe_tensor* gate_b = nullptr) {
   try {
     if (!inputs || n < 0 || n > 64) return fail(MOE_INVALID_ARGUMENT, "bad inputs");
     moe_tensor local[64];
     moe_status st = with_packed(kernel, inputs, n, local);
     if (st != MOE_OK) return st;
+    if (gate_w && (st = gate_router_input(gate_w, gate_b, local, n)) != MOE_OK) return st;
     Problem p;
     st = validate(kernel, local, n, &p);
     if (st != MOE_OK) return st;
@@ -626,6 +661,13 @@ moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int3
     ra.p.scratch_bytes = l.route_scratch_bytes;
     ra.tile_offsets = reinterpret_cast<int32_t*>(ws + l.tile_offsets);
     ra.tile_m = moe::kPrefillTileM;
+    if (gate_w) {
+      ra.p.logits = ws + l.logits;
+      ra.gate_x = p.in[0]->data;
+      ra.gate_w = gate_w->data;
+      ra.gate_b = gate_b ? gate_b->data : nullptr;
+      ra.hidden = p.H;
+    }
     moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
     if (p.gate_mode == moe::kGateFc3 && (kernel->packed[2].data != nullptr) != (kernel->packed[8].data != nullptr))
       return fail(MOE_NOT_IMPLEMENTED, "fc1 and fc3 weights must both be pre-packed or neither");
@@ -650,7 +692,7 @@ moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int3
       if (e != hipSuccess) failed_stage = name;
     };
     // small decode batches are routed inside the fc1 kernel (one launch less)
-    const bool route_in_fc1 = path == moe::kPathDecode && moe::decode_routes_in_fc1(a);
+    const bool route_in_fc1 = !gate_w && path == moe::kPathDecode && moe::decode_routes_in_fc1(a);
     mark(0);
     if (!route_in_fc1) {
       e = e == hipSuccess ? moe::launch_route_dispatch(ra, stream) : e;
@@ -755,6 +797,27 @@ moe_status moe_kernel_compute(const moe_kernel* kernel, const moe_tensor* inputs
     std::fprintf(stderr, "MOE_KERNEL_END %s kernel=%p path=%d status=%d%s%s\n", kernel->quantized ? "QMoE" : "MoE",
                  static_cast<const void*>(kernel), kernel->last_path, static_cast<int>(st),
                  st == MOE_OK ? "" : " ", st == MOE_OK ? "" : g_last_error.c_str());
+    std::fflush(stderr);
+  }
+  return st;
+}
+
+moe_status moe_kernel_compute_fused_router(const moe_kernel* kernel, const moe_tensor* inputs, int32_t n,
+                                          const moe_tensor* router_weight, const moe_tensor* router_bias,
+                                          void* output, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!kernel) return fail(MOE_INVALID_ARGUMENT, "null kernel");
+  if (!router_weight) return fail(MOE_INVALID_ARGUMENT, "router_weight is required");
+  if (kernel->trace) {
+    std::fprintf(stderr, "MOE_KERNEL_BEGIN %s+router kernel=%p\n", kernel->quantized ? "QMoE" : "MoE",
+                 static_cast<const void*>(kernel));
+    std::fflush(stderr);
+  }
+  const moe_status st = compute_impl(kernel, inputs, n, output, workspace, workspace_bytes, stream, router_weight,
+                                     router_bias && router_bias->data ? router_bias : nullptr);
+  if (kernel->trace) {
+    std::fprintf(stderr, "MOE_KERNEL_END %s+router kernel=%p path=%d status=%d%s%s\n",
+                 kernel->quantized ? "QMoE" : "MoE", static_cast<const void*>(kernel), kernel->last_path,
+                 static_cast<int>(st), st == MOE_OK ? "" : " ", st == MOE_OK ? "" : g_last_error.c_str());
     std::fflush(stderr);
   }
   return st;

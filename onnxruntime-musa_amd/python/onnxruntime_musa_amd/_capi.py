@@ -53,7 +53,7 @@ class MoeTensor(ctypes.Structure):
 
 class MoeWorkspaceLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in ("topk_ids", "topk_w", "offsets", "perm", "inv_perm", "total",
-                                               "act", "y2", "y2_planes_max")]
+                                               "act", "y2", "y2_planes_max", "logits")]
 
 
 class MoeRouteParams(ctypes.Structure):
@@ -115,6 +115,10 @@ EXPORTS = [
     ("moe_kernel_compute", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     ("moe_kernel_release", None, [ctypes.c_void_p]),
+    ("moe_kernel_compute_fused_router", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
+                                                       ctypes.POINTER(MoeTensor), ctypes.POINTER(MoeTensor),
+                                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                                       ctypes.c_void_p]),
     ("moe_kernel_compute_noalloc", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,
                                                   ctypes.c_void_p, ctypes.c_void_p]),
     ("moe_kernel_workspace_layout", ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(MoeTensor), ctypes.c_int32,

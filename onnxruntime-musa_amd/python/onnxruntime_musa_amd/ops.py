@@ -181,6 +181,50 @@ class _MoEOp:
                                            ws_bytes, ctypes.c_void_p(s.cuda_stream)))
         return out
 
+    def fused_router(self, *inputs, router_weight: torch.Tensor, router_bias: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+                     stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """The op with the router GEMM fused (moe_kernel_compute_fused_router):
+        inputs in schema order with router_probs None; router_weight [E, H]
+        (the transposed MatMul operand), router_bias [E] or None."""
+        x = inputs[0]
+        if inputs[1] is not None:
+            raise ValueError("router_probs must be None: the fused router computes the logits")
+        arr, n = self._descs(inputs)
+        s = stream if stream is not None else torch.cuda.current_stream(x.device)
+        if out is None:
+            with torch.cuda.stream(s):
+                out = torch.empty_like(x)
+        elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("out must match the input's shape and dtype")
+        wd = _tensor_desc(router_weight)
+        bd = _tensor_desc(router_bias)
+        ws_ptr, ws_bytes = None, 0
+        if workspace is not None:
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        check(self._lib.moe_kernel_compute_fused_router(self._h, arr, n, ctypes.byref(wd), ctypes.byref(bd),
+                                                        out.data_ptr() if out.numel() else None, ws_ptr, ws_bytes,
+                                                        ctypes.c_void_p(s.cuda_stream)))
+        return out
+
+    def bind_fused_router(self, *inputs, router_weight: torch.Tensor, router_bias: Optional[torch.Tensor] = None,
+                          out: torch.Tensor, workspace: torch.Tensor, stream: Optional[torch.cuda.Stream] = None):
+        """bind() for the fused router: a zero-argument callable that enqueues
+        one moe_kernel_compute_fused_router on fixed buffers."""
+        arr, n = self._descs(inputs)
+        s = stream if stream is not None else torch.cuda.current_stream(inputs[0].device)
+        wd, bd = _tensor_desc(router_weight), _tensor_desc(router_bias)
+        fn = self._lib.moe_kernel_compute_fused_router
+        args = (self._h, arr, n, ctypes.byref(wd), ctypes.byref(bd), ctypes.c_void_p(out.data_ptr()),
+                ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
+                ctypes.c_void_p(s.cuda_stream))
+        keep = (inputs, router_weight, router_bias, out, workspace, wd, bd)
+
+        def call():
+            check(fn(*args))
+            return keep[3]
+        return call
+
     def compute_noalloc(self, *inputs, out: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         """The op on the library's static scratch (moe_kernel_compute_noalloc):
         no device allocation, for callers that cannot allocate.  `out` is

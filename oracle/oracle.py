@@ -130,6 +130,40 @@ def softmax(x: np.ndarray, axis: int = -1) -> np.ndarray:
     return e * (1.0 / np.sum(e, axis=axis, keepdims=True))
 
 
+def gate_logits(x: np.ndarray, w: np.ndarray, b: Optional[np.ndarray], dtype: str) -> np.ndarray:
+    """Router GEMM restated: logits[t, e] = sum_h x[t, h] w[e, h] (+ b[e]),
+    evaluated in float64 and rounded once to the activation type -- what the
+    graph's MatMul(x, W[H, E]) (+ Add) feeding the MoE node stores.  Arrays
+    are in their storage types (bf16 as uint16); returns the same type."""
+    xf = to_f32(x, dtype).astype(np.float64)
+    wf = to_f32(w, dtype).astype(np.float64)
+    lg = xf @ wf.T
+    if b is not None:
+        lg = lg + to_f32(b, dtype).astype(np.float64)
+    if dtype == "bf16":
+        # RNE of the float64 value: via float32 is exact here only when the
+        # float32 rounding is not itself a tie; a direct RNE avoids that
+        return f64_to_bf16_bits(lg)
+    if dtype == "f16":
+        return lg.astype(np.float16)
+    return lg.astype(np.float32)
+
+
+def f64_to_bf16_bits(v: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 bits, round to nearest even (one rounding)."""
+    v = np.asarray(v, np.float64)
+    f = v.astype(np.float32)  # nearest float32 (RNE)
+    bits = f.view(np.uint32).astype(np.uint64)
+    up = (bits + np.uint64(0x10000)) & np.uint64(0xFFFF0000)
+    down = bits & np.uint64(0xFFFF0000)
+    vu = up.astype(np.uint32).view(np.float32).astype(np.float64)
+    vd = down.astype(np.uint32).view(np.float32).astype(np.float64)
+    du, dd = np.abs(vu - v), np.abs(vd - v)
+    pick_up = (du < dd) | ((du == dd) & (((down >> np.uint64(16)) & np.uint64(1)) == 1))
+    out = np.where(pick_up, up, down) >> np.uint64(16)
+    return out.astype(np.uint16)
+
+
 def dispatch(ids: np.ndarray, E: int):
     """ids [T, k] -> (offsets [E+1], perm [T*k])."""
     ids = np.ascontiguousarray(ids, dtype=np.int32)

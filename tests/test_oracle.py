@@ -674,3 +674,31 @@ def test_softmax_oracle_closed_forms():
     ids, _ = oracle.route(lg, 8, False, False)
     np.testing.assert_allclose(w, np.take_along_axis(oracle.softmax(lg.astype(np.float64), -1), ids, axis=-1),
                                rtol=1e-5)
+
+
+# ---- router GEMM restatement (oracle.gate_logits): a float64 matmul
+# rounded once to the activation type, pinned by exact integer arithmetic and
+# by the rounding of the types ----
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_gate_logits_exact_integer_products(dtype):
+    rng = np.random.default_rng(21)
+    T, H, E = 7, 96, 9
+    xi = rng.integers(-3, 4, size=(T, H))
+    wi = rng.integers(-4, 5, size=(E, H))
+    bi = rng.integers(-5, 6, size=E)
+    cast = {"f32": lambda a: a.astype(np.float32), "f16": lambda a: a.astype(np.float16),
+            "bf16": lambda a: oracle.f32_to_bf16_bits(a.astype(np.float32))}[dtype]
+    got = oracle.to_f32(oracle.gate_logits(cast(xi), cast(wi), cast(bi), dtype), dtype)
+    exact = (xi @ wi.T + bi).astype(np.float64)          # integers below 2^8: exact in every type
+    np.testing.assert_array_equal(got.astype(np.float64), exact)
+
+
+def test_gate_logits_round_once():
+    # a value between two bf16 neighbours rounds to the nearer one, a tie to even
+    x = oracle.f32_to_bf16_bits(np.array([[1.0, 1.0]], np.float32))
+    w = oracle.f32_to_bf16_bits(np.array([[1.0, 2.0 ** -8], [1.0, 3 * 2.0 ** -9]], np.float32))
+    got = oracle.to_f32(oracle.gate_logits(x, w, None, "bf16"), "bf16")
+    # 1 + 2^-8 is halfway between 1 and 1 + 2^-7: ties to even (1); 1 + 3 2^-9 rounds up
+    np.testing.assert_array_equal(got, [[1.0, 1.0 + 2.0 ** -7]])
+    # a planted double rounding (float64 -> float32 -> bf16 without care) is not what the oracle does
+    assert oracle.f64_to_bf16_bits(np.array([1.0 + 2.0 ** -8 + 2.0 ** -40]))[0] == 0x3F81
