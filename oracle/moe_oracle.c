@@ -182,6 +182,34 @@ int orc_dequant(const uint8_t *q, const void *scales, int32_t scale_dtype, int32
   return 0;
 }
 
+/* MXFP4 per the OCP Microscaling Formats (MX) v1.0 specification: an FP4
+ * E2M1 element (sign, 2 exponent bits with bias 1, 1 mantissa bit; exponent
+ * 0 is subnormal: 0 or 0.5) times the block's E8M0 scale (2^(e - 127), the
+ * byte 0xFF encoding NaN).  Public format (openai/gpt-oss ships its expert
+ * weights in it); no reference file restates it. */
+float orc_e2m1_to_f32(uint32_t nib) {
+  const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
+  const float mag = e == 0 ? 0.5f * (float)m : ldexpf(1.0f + 0.5f * (float)m, (int)e - 1);
+  return (nib & 8u) ? -mag : mag;
+}
+
+float orc_e8m0_to_f32(uint32_t e) { return e == 255u ? NAN : ldexpf(1.0f, (int)e - 127); }
+
+static void dequant_row_mxfp4(const uint8_t *q, const uint8_t *scales, int64_t n, int64_t K, float *out) {
+  const uint8_t *r = q + n * (K / 2);
+  const uint8_t *s = scales + n * (K / 32);
+  for (int64_t kk = 0; kk < K; ++kk) {
+    const uint32_t nib = (kk & 1) ? (r[kk >> 1] >> 4) : (r[kk >> 1] & 0x0F);
+    out[kk] = orc_e2m1_to_f32(nib) * orc_e8m0_to_f32(s[kk / 32]);
+  }
+}
+
+int orc_dequant_mxfp4(const uint8_t *q, const uint8_t *scales, int64_t N, int64_t K, float *out) {
+  if (K % 32) return 1;
+  for (int64_t n = 0; n < N; ++n) dequant_row_mxfp4(q, scales, n, K, out + n * K);
+  return 0;
+}
+
 /* Weight row n of one expert matrix [N, K] as fp32. */
 static void weight_row(const orc_moe_args *a, const void *w, const void *s, int64_t e,
                        int64_t N, int64_t K, int64_t n, float *out) {
@@ -191,6 +219,10 @@ static void weight_row(const orc_moe_args *a, const void *w, const void *s, int6
     return;
   }
   const int64_t row_bytes = a->quant_bits == 8 ? K : K / 2;
+  if (a->weight_format == 1) {
+    dequant_row_mxfp4((const uint8_t *)w + e * N * row_bytes, (const uint8_t *)s + e * N * (K / 32), n, K, out);
+    return;
+  }
   const int64_t nblk = a->block_size > 0 ? K / a->block_size : 1;
   const uint8_t *qe = (const uint8_t *)w + e * N * row_bytes;
   const int64_t soff = e * N * nblk;
@@ -252,6 +284,7 @@ int orc_moe_forward(const orc_moe_args *a) {
   if (a->quant_bits != 0 && a->quant_bits != 4 && a->quant_bits != 8) return 1;
   if (a->quant_bits == 4 && ((H & 1) || (I & 1))) return 1;
   if (a->block_size > 0 && (H % a->block_size || I % a->block_size)) return 1;
+  if (a->weight_format == 1 && (a->quant_bits != 4 || a->block_size != 32)) return 1;
   const int gated3 = a->w3 != NULL;
   const int fused = (a->activation == ORC_ACT_SWIGLU && !gated3);
   if (fused && a->swiglu_fusion != 1 && a->swiglu_fusion != 2) return 1;

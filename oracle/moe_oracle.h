@@ -72,6 +72,8 @@ typedef struct {
   float *out_f32;             /* [T, H] fp32 result before rounding to T */
   const uint8_t *token_mask;  /* [T]; if set, only tokens with mask != 0 are computed */
   int32_t num_threads;        /* <= 0: OpenMP default */
+  int32_t weight_format;      /* 0: integer, zero point 128 / 8 (QMoE); 1: MXFP4 (quant_bits 4,
+                                 block_size 32, scales uint8 E8M0) */
 } orc_moe_args;
 
 /* Full forward.  Returns 0 on success, nonzero on a bad argument. */
@@ -88,6 +90,13 @@ int orc_dispatch(const int32_t *ids, int64_t T, int64_t k, int64_t E, int32_t *o
 /* Dequantize one expert matrix [N, K] to fp32. */
 int orc_dequant(const uint8_t *q, const void *scales, int32_t scale_dtype, int32_t bits,
                 int64_t block_size, int64_t N, int64_t K, float *out);
+
+/* MXFP4 (OCP Microscaling Formats v1.0: FP4 E2M1 elements, two per byte,
+ * even k in the low nibble; one E8M0 scale byte per 32 elements along K):
+ * w = e2m1(nibble) * 2^(scale - 127), scale 0xFF = NaN.  [N, K] to fp32. */
+int orc_dequant_mxfp4(const uint8_t *q, const uint8_t *scales, int64_t N, int64_t K, float *out);
+float orc_e2m1_to_f32(uint32_t nibble);
+float orc_e8m0_to_f32(uint32_t e);
 
 /* Activation on one fc1 row (fp32), writing I values.  For fused SwiGLU h1 has
  * 2I entries; for fc3 gating h3 holds the linear half. */

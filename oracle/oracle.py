@@ -38,7 +38,7 @@ class OrcArgs(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("topk_ids", ctypes.c_void_p), ("topk_w", ctypes.c_void_p), ("expert_offsets", ctypes.c_void_p),
         ("perm", ctypes.c_void_p), ("out_f32", ctypes.c_void_p), ("token_mask", ctypes.c_void_p),
-        ("num_threads", ctypes.c_int32),
+        ("num_threads", ctypes.c_int32), ("weight_format", ctypes.c_int32),
     ]
 
 
@@ -62,6 +62,13 @@ def load():
         lib.orc_dequant.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
         lib.orc_dequant.restype = ctypes.c_int
+        lib.orc_dequant_mxfp4.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                          ctypes.c_void_p]
+        lib.orc_dequant_mxfp4.restype = ctypes.c_int
+        lib.orc_e2m1_to_f32.argtypes = [ctypes.c_uint32]
+        lib.orc_e2m1_to_f32.restype = ctypes.c_float
+        lib.orc_e8m0_to_f32.argtypes = [ctypes.c_uint32]
+        lib.orc_e8m0_to_f32.restype = ctypes.c_float
         lib.orc_activation.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
                                        ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                        ctypes.c_void_p]
@@ -185,6 +192,16 @@ def dequant(q: np.ndarray, scales: np.ndarray, scale_dtype: str, bits: int, bloc
     return out
 
 
+def dequant_mxfp4(q: np.ndarray, scales: np.ndarray, N: int, K: int) -> np.ndarray:
+    """MXFP4 [N, K/2] bytes + [N, K/32] E8M0 scale bytes -> fp32 [N, K]."""
+    out = np.zeros((N, K), np.float32)
+    rc = load().orc_dequant_mxfp4(_ptr(np.ascontiguousarray(q, np.uint8)), _ptr(np.ascontiguousarray(scales, np.uint8)),
+                                  N, K, _ptr(out))
+    if rc:
+        raise ValueError(f"orc_dequant_mxfp4 rc={rc}")
+    return out
+
+
 def activation(h1: np.ndarray, h3: Optional[np.ndarray], inter: int, act: str, fusion: int = 0,
                alpha: float = 1.0, beta: float = 0.0, limit: float = float("inf")) -> np.ndarray:
     h1 = np.ascontiguousarray(h1, dtype=np.float32)
@@ -197,7 +214,7 @@ def activation(h1: np.ndarray, h3: Optional[np.ndarray], inter: int, act: str, f
 def moe_forward(*, x, logits, w1, w2, k, hidden, inter, experts, act_dtype="f32", activation="relu",
                 normalize=0, swiglu_fusion=0, swiglu_limit=None, alpha=1.0, beta=0.0, router_sigmoid=0,
                 bits=0, block_size=0, scale_dtype="f16", s1=None, b1=None, s2=None, b2=None, w3=None,
-                s3=None, b3=None, token_mask=None, threads=0):
+                s3=None, b3=None, token_mask=None, threads=0, weight_format=0):
     """Runs the restated op.  Arrays are numpy in their storage types (bf16 as
     uint16).  Returns dict(out, out_f32, topk_ids, topk_w, offsets, perm)."""
     T = x.shape[0]
@@ -237,6 +254,7 @@ def moe_forward(*, x, logits, w1, w2, k, hidden, inter, experts, act_dtype="f32"
     if token_mask is not None:
         a.token_mask = c(np.asarray(token_mask, dtype=np.uint8))
     a.num_threads = int(threads)
+    a.weight_format = int(weight_format)
     rc = load().orc_moe_forward(ctypes.byref(a))
     if rc:
         raise ValueError(f"orc_moe_forward rc={rc}")
@@ -254,7 +272,8 @@ def forward_problem(cfg, host: dict, token_mask=None, threads=0):
         router_sigmoid=getattr(cfg, "router_sigmoid", 0), bits=cfg.bits, block_size=cfg.block_size,
         scale_dtype=cfg.scale_dtype, s1=host.get("fc1_scales"), b1=host.get("fc1_experts_bias"),
         s2=host.get("fc2_scales"), b2=host.get("fc2_experts_bias"), w3=host.get("fc3_experts_weights"),
-        s3=host.get("fc3_scales"), b3=host.get("fc3_experts_bias"), token_mask=token_mask, threads=threads)
+        s3=host.get("fc3_scales"), b3=host.get("fc3_experts_bias"), token_mask=token_mask, threads=threads,
+        weight_format=1 if getattr(cfg, "weight_format", "int") == "mxfp4" else 0)
 
 
 def f16_bits_to_f32(u16: np.ndarray) -> np.ndarray:

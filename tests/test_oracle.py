@@ -334,6 +334,124 @@ def test_planted_encoding_mistakes_fail_round_trip(bits, block):
         assert _round_trip_excess(bad, w, s) > 1.5, "block scales along N"
 
 
+# ---------------------------------------------------------------- MXFP4
+# OCP Microscaling Formats (MX) v1.0: FP4 E2M1 elements (1 sign, 2 exponent
+# bits with bias 1, 1 mantissa bit), E8M0 block scales of 32 elements.
+E2M1_GRID = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0])
+
+
+def test_e2m1_and_e8m0_known_answers():
+    lib = oracle.load()
+    got = [lib.orc_e2m1_to_f32(n) for n in range(16)]
+    assert got[:8] == list(E2M1_GRID)
+    assert got[8:] == list(-E2M1_GRID)
+    assert math.copysign(1.0, got[8]) == -1.0                  # 0b1000 is -0
+    for e, v in ((127, 1.0), (128, 2.0), (126, 0.5), (0, 2.0 ** -127), (254, 2.0 ** 127), (137, 1024.0)):
+        assert lib.orc_e8m0_to_f32(e) == v, e
+    assert math.isnan(lib.orc_e8m0_to_f32(255))
+
+
+def test_mxfp4_hand_packed_bytes():
+    """One row, K = 64: two scale blocks.  Even k is the low nibble."""
+    q = np.zeros((1, 32), np.uint8)
+    q[0, 0] = 0x2F          # k0 = -6 (0xF), k1 = +1 (0x2)
+    q[0, 1] = 0x90          # k2 = 0, k3 = -0.5 (0x9)
+    q[0, 16] = 0x71         # k32 = 0.5, k33 = 6
+    s = np.array([[128, 125]], np.uint8)                       # 2 and 1/4
+    d = oracle.dequant_mxfp4(q, s, 1, 64)[0]
+    assert list(d[:4]) == [-12.0, 2.0, 0.0, -1.0]
+    assert list(d[32:34]) == [0.125, 1.5]
+    assert not d[4:32].any() and not d[34:].any()
+    nan = oracle.dequant_mxfp4(q, np.array([[255, 127]], np.uint8), 1, 64)[0]
+    assert np.isnan(nan[:32]).all() and list(nan[32:34]) == [0.5, 6.0]
+
+
+def _spec_quantize_mxfp4(w: np.ndarray):
+    """The MX v1.0 quantizer (section 6.3): shared exponent
+    floor(log2(max|w|)) - 2 (E2M1's largest exponent), elements rounded to the
+    nearest E2M1 value (ties to the even mantissa) and clamped to +-6."""
+    N, K = w.shape
+    wb = w.astype(np.float64).reshape(N, K // 32, 32)
+    amax = np.abs(wb).max(axis=2)
+    e = np.where(amax > 0, np.floor(np.log2(np.where(amax > 0, amax, 1))) - 2, -127).astype(np.int64)
+    X = np.ldexp(1.0, e)[:, :, None]
+    a = np.minimum(np.abs(wb) / X, 6.0)
+    dist = np.abs(a[..., None] - E2M1_GRID)                    # nearest grid point; ties -> even code
+    best = dist.min(-1, keepdims=True)
+    cand = np.where(dist == best, np.arange(8), 99)
+    even = np.where(cand % 2 == 0, cand, 99).min(-1)
+    code = np.where(even < 99, even, cand.min(-1))
+    nib = (code | np.where(wb < 0, 8, 0)).reshape(N, K).astype(np.uint8)
+    q = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    return q, (e + 127).astype(np.uint8), np.broadcast_to(X, wb.shape).reshape(N, K)
+
+
+def _mxfp4_excess(d: np.ndarray, w: np.ndarray, X: np.ndarray) -> float:
+    """max |d - w| over the nearest-value bound: half the grid step at |w|/X
+    (0.25, 0.5, 1 for [0,2), [2,4), [4,6]) and the clamp distance past 6."""
+    a = np.abs(w.astype(np.float64)) / X
+    half = np.where(a < 2, 0.25, np.where(a < 4, 0.5, 1.0))
+    bound = np.maximum(half, a - 6.0) * X
+    return float(np.max(np.abs(d.astype(np.float64) - w) / bound))
+
+
+def test_mxfp4_quantizer_round_trip_and_planted_mistakes():
+    N, K = 16, 256
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((N, K)) * np.array([1e-3, 1.0, 40.0, 3e4])[rng.integers(0, 4, (N, 1))]).astype(np.float32)
+    q, s, X = _spec_quantize_mxfp4(w)
+    good = oracle.dequant_mxfp4(q, s, N, K)
+    assert _mxfp4_excess(good, w, X) <= 1.0 + 1e-9
+    # each block's largest element lands in [4, 6] x X, the top binade
+    top = np.abs(good.reshape(N, K // 32, 32)).max(2) / X.reshape(N, K // 32, 32)[:, :, 0]
+    assert ((top >= 4) & (top <= 6)).all()
+    mutants = {"high nibble first": (((q & 0x0F) << 4) | (q >> 4)).astype(np.uint8),
+               "sign bit as mantissa": (q ^ 0x99).astype(np.uint8)}
+    for what, qm in mutants.items():
+        assert _mxfp4_excess(oracle.dequant_mxfp4(qm, s, N, K), w, X) > 1.5, what
+    assert _mxfp4_excess(oracle.dequant_mxfp4(q, (s + 1).astype(np.uint8), N, K), w, X) > 1.5, "scale bias 126"
+    assert _mxfp4_excess(oracle.dequant_mxfp4(q, (s - 1).astype(np.uint8), N, K), w, X) > 1.5, "scale bias 128"
+
+
+def test_mxfp4_forward_matches_float64_formulation():
+    """The forward with MXFP4 experts against a dense float64 restatement that
+    decodes with numpy's own table (E2M1_GRID, 2.0 ** (s - 127))."""
+    T, H, I, E, k = 12, 64, 32, 4, 2
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    q1, s1, _ = zip(*[_spec_quantize_mxfp4(rng.standard_normal((2 * I, H)).astype(np.float32) / 8) for _ in range(E)])
+    q2, s2, _ = zip(*[_spec_quantize_mxfp4(rng.standard_normal((H, I)).astype(np.float32) / 8) for _ in range(E)])
+    q1, s1, q2, s2 = map(np.stack, (q1, s1, q2, s2))
+    b1 = rng.standard_normal((E, 2 * I)).astype(np.float32)
+    b2 = rng.standard_normal((E, H)).astype(np.float32)
+    r = oracle.moe_forward(x=x, logits=lg, w1=q1, w2=q2, k=k, hidden=H, inter=I, experts=E, activation="swiglu",
+                           swiglu_fusion=1, swiglu_limit=7.0, alpha=1.702, beta=1.0, normalize=1, bits=4,
+                           block_size=32, scale_dtype="f32", s1=s1, b1=b1, s2=s2, b2=b2, weight_format=1)
+
+    def deq(qe, se):
+        nib = np.stack([qe & 0x0F, qe >> 4], -1).reshape(qe.shape[0], -1)
+        val = np.where(nib & 8, -1.0, 1.0) * E2M1_GRID[nib & 7]
+        return val * np.repeat(2.0 ** (se.astype(np.float64) - 127), 32, axis=1)
+
+    p = np.exp(lg - lg.max(1, keepdims=True))
+    order = np.argsort(-lg, axis=1, kind="stable")[:, :k]
+    wsel = np.take_along_axis(p, order, 1)
+    wsel /= wsel.sum(1, keepdims=True)
+    ref = np.zeros((T, H))
+    for e in range(E):
+        tok, slot = np.nonzero(order == e)
+        h1 = x[tok].astype(np.float64) @ deq(q1[e], s1[e]).T + b1[e]
+        g, l = np.minimum(h1[:, 0::2], 7.0), np.clip(h1[:, 1::2], -7.0, 7.0)
+        a = g / (1 + np.exp(-1.702 * g)) * (l + 1.0)
+        y = a @ deq(q2[e], s2[e]).T + b2[e]
+        ref[tok] += wsel[tok, slot][:, None] * y
+    np.testing.assert_allclose(r["out_f32"], ref, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError):
+        oracle.moe_forward(x=x, logits=lg, w1=q1, w2=q2, k=k, hidden=H, inter=I, experts=E, activation="swiglu",
+                           swiglu_fusion=1, bits=4, block_size=16, scale_dtype="f32", s1=s1, s2=s2, weight_format=1)
+
+
 # ---------------------------------------------------------------- activations
 def test_activation_closed_forms():
     h = np.array([1.0, -2.0, 0.5], np.float32)
