@@ -229,13 +229,18 @@ MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
  * constant initializer on the device) are reordered once into a tile-major
  * layout: each 16 rows x 128 k of an expert's [N, K/pack] matrix become one
  * contiguous block (1 KB int4, 2 KB int8), so that every load instruction
- * of the decode kernels reads one 1 KB run.  act_type is the op's input
- * element type T (known from the node at kernel creation).
+ * of the decode kernels reads one 1 KB run; K is padded with zeros to whole
+ * chunks of 128, and the fused fc1 of interleaved SwiGLU is stored with its
+ * gate rows first and its linear rows after.  Block scales of block size 32
+ * or 64 (input_index 3 fc1, 6 fc2, 9 fc3; int4, or int8 with fp16
+ * activations) are packed the same way, the 16 rows' scales of each chunk
+ * contiguous; they need their weights packed too.  act_type is the op's
+ * input element type T (known from the node at kernel creation).
  *
  * moe_kernel_prepack_size: bytes of the packed copy, or 0 when the kernel
  *   reads that input in the op's layout (MoE, fp32 activations, N not a
- *   multiple of 16, K not a multiple of 128, interleaved SwiGLU fc1, fc1/fc3
- *   K above 4096).
+ *   multiple of 16 (32 for a fused fc1), rows not whole 16-byte pieces,
+ *   fc1/fc3 K above 4096, scales of other block sizes).
  * moe_kernel_prepack: writes the packed copy into dst (device, at least that
  *   many bytes, 16-byte aligned) on stream, records dst and sets *is_packed.
  *   Every later compute (and workspace query) reads that input from dst; the
@@ -245,8 +250,9 @@ MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
  *   the pack.  A later call that passes a tensor for a packed input must
  *   pass the one that was packed (same data pointer) or dst itself;
  *   another tensor, even of the same shape, is MOE_INVALID_ARGUMENT.  fc1
- *   and fc3 are packed together or not at all.  Call before the kernel is
- *   shared between threads. */
+ *   and fc3 are packed together or not at all, and packed scales need
+ *   packed weights (else compute returns MOE_NOT_IMPLEMENTED).  Call before
+ *   the kernel is shared between threads. */
 MOE_API moe_status moe_kernel_prepack_size(const moe_kernel *kernel, int32_t input_index,
                                            const moe_tensor *weights, int32_t act_type, size_t *bytes);
 MOE_API moe_status moe_kernel_prepack(moe_kernel *kernel, int32_t input_index, const moe_tensor *weights,

@@ -62,7 +62,10 @@ __device__ __forceinline__ u32x4_t bload16_aux(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, AUX));
 }
 
-enum ScaleMode : int { kScaleNone = 0, kScaleChan = 1, kScaleBlock = 2, kScaleFold = 3 };
+// kScaleStep (stream kernel, block 32 / 64): each MFMA step takes 32
+// consecutive k, which lie in one scale block, so the operands stay exact
+// (biased) integers and the block scale multiplies the step's fp32 result.
+enum ScaleMode : int { kScaleNone = 0, kScaleChan = 1, kScaleBlock = 2, kScaleFold = 3, kScaleStep = 4 };
 
 struct Stage {
   const void* in;  // fc1: x [T, K]; fc2: act [T*k, K]
@@ -79,7 +82,11 @@ struct Stage {
   int32_t gate_mode, scale_type, activation, ks;
   int32_t ksg;        // K splits across workgroups (fc2 only)
   int32_t lds_scale;  // bytes of LDS per wave for staged scales
-  int32_t tiled;      // weights tile-major (stream kernel only)
+  int32_t tiled;      // weights tile-major (stream kernel only; K padded to whole chunks)
+  int32_t deint;      // fc1 tile-major weights of interleaved SwiGLU stored de-interleaved:
+                      // gate rows [0, nfeat), linear rows [nfeat, 2 nfeat); scales and
+                      // biases keep the interleaved order
+  int32_t stiled;     // step-scale block scales tile-major (stream kernel; rows as the weights')
   int64_t block_size;
   float alpha, beta, limit;
   const int32_t* offsets;

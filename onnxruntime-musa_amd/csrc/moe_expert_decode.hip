@@ -152,6 +152,8 @@ decode::Stage fc1_stage(const ExpertArgs& a) {
   st.out = a.act;
   st.out_rows = a.T * a.k;
   st.tiled = a.tiled1;
+  st.deint = a.deint1;
+  st.stiled = a.stiled1;
   return st;
 }
 
@@ -179,6 +181,7 @@ decode::Stage fc2_stage(const ExpertArgs& a) {
   st.out = a.y2;
   st.out_rows = a.T * a.k;
   st.tiled = a.tiled2;
+  st.stiled = a.stiled2;
   return st;
 }
 

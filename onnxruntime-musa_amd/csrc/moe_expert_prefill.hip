@@ -89,7 +89,9 @@ struct PStage {
   int32_t ksplit;   // K splits (partial planes of the output)
   int32_t out_half; // fc2 with one plane: y2 stored in the activation type
   int32_t kstages;  // stages per K split
-  int32_t tiled;    // weights tile-major (int4 / int8)
+  int32_t tiled;    // weights tile-major (int4 / int8), K padded to whole stages
+  int32_t deint;    // fused interleaved fc1 stored de-interleaved (gate rows, then linear rows)
+  int32_t stiled;   // block scales (block 32 / 64) tile-major, rows as the weights
   int64_t out_rows;
   void* out;  // fc1: act [rows, nfeat] (AT); fc2: y2 [ksplit][rows, nfeat] fp32
 };
@@ -148,13 +150,18 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   // uniform, so one VGPR offset per lane serves both blocks (the rest rides in
   // the scalar offset).  Rows of features past nfeat are read (past the
   // buffer: zeros) but their outputs are never stored. ----
-  const int64_t rb = static_cast<int64_t>(K) * G::EBITS / 8;  // bytes of one weight row
+  // bytes of one weight row (tile-major: K padded to whole stages of BK)
+  const bool tiled = WF != kDense && p.tiled != 0;
+  const int64_t rb = tiled ? static_cast<int64_t>((K + BK - 1) / BK) * BK * G::EBITS / 8
+                           : static_cast<int64_t>(K) * G::EBITS / 8;
   const uint8_t* wbase_g = p.w + static_cast<int64_t>(e) * p.w_rows * rb;
   const uint8_t* wbase_l = p.wl + static_cast<int64_t>(e) * p.wl_rows * rb;
   const __amdgpu_buffer_rsrc_t rs_g = make_rsrc(wbase_g, static_cast<uint32_t>(p.w_rows * rb));
   const __amdgpu_buffer_rsrc_t rs_l = make_rsrc(wbase_l, static_cast<uint32_t>(p.wl_rows * rb));
   const int64_t fl = GATED ? static_cast<int64_t>(ntile) * (BN / 2) + wave * 32 + lr
                            : static_cast<int64_t>(ntile) * BN + wave * 64 + lr;
+  // row0 / drow: rows of the scales and biases; wrow0 / wdrow: weight rows
+  // (the same, unless a fused interleaved fc1 is stored de-interleaved)
   const bool interleaved = GATED && p.gate_mode == kGateInterleaved;
   const int64_t row0 = interleaved ? 2 * fl : fl;
   int64_t drow[kNT];
@@ -165,18 +172,22 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
     drow[0] = 0;
     drow[1] = 32;
   }
+  const bool deint = interleaved && tiled && p.deint != 0;
+  const int64_t wrow0 = deint ? fl : row0;
+  int64_t wdrow[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) wdrow[j] = deint ? (j == 0 ? 0 : p.nfeat) : drow[j];
   // Tile-major weights (pre-packed, int4 / int8; a stage is one chunk of
   // 128 k): the 16 rows x 128 k of a weight tile and chunk are one block of
   // CB bytes in which piece q (16 bytes) of row r sits at ((q % kv) * 64 + (q
   // / kv) * 16 + r) * 16, kv = 16-byte vectors per 32 k.  Lane half h reads
-  // pieces BVEC h .. BVEC h + BVEC - 1 of its row.  drow steps (0, 32, nfeat)
-  // are whole tiles, so they stay row offsets.
+  // pieces BVEC h .. BVEC h + BVEC - 1 of its row.  wdrow steps (0, 32,
+  // nfeat) are whole tiles, so they stay row offsets.
   constexpr int kKv = WF == kInt8 ? 2 : 1;
   constexpr int CB = 1024 * kKv;
-  const bool tiled = WF != kDense && p.tiled != 0;
   const uint32_t woff =
-      tiled ? static_cast<uint32_t>((row0 / 16) * 16 * rb + (row0 % 16) * 16 + static_cast<int64_t>(kbeg / BK) * CB + 512 * h)
-            : static_cast<uint32_t>(row0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
+      tiled ? static_cast<uint32_t>((wrow0 / 16) * 16 * rb + (wrow0 % 16) * 16 + static_cast<int64_t>(kbeg / BK) * CB + 512 * h)
+            : static_cast<uint32_t>(wrow0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
   const int cstride = tiled ? CB : BK * G::EBITS / 8;  // weight bytes per stage
   // offset of vector v beyond 16 v (tiled: piece BVEC h + v)
   int vdelta[BVEC];
@@ -193,18 +204,42 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   constexpr int WB = 16 / SB;  // blocks per window
   const int bshift = kFold ? __builtin_ctzll(static_cast<uint64_t>(p.block_size)) : 0;
   const int nblk = kFold ? (K >> bshift) : 0;
+  // Tile-major scales (pre-packed for the decode kernels, block 32 / 64):
+  // per (16-row tile, chunk of 128 k) the 16 rows' nbc = 128 / block scales;
+  // nblk_r elements per row with K padded to whole chunks.  A window of WB
+  // blocks is then WB / nbc pieces of nbc * SB bytes, one per chunk.
+  const bool stiled = kFold && p.stiled != 0;
+  const int nbc = 128 >> bshift;
+  const int nblk_r = stiled ? (K + 127) / 128 * nbc : nblk;
   const __amdgpu_buffer_rsrc_t rs_sg =
-      make_rsrc(kFold ? static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk * SB : nullptr,
-                static_cast<uint32_t>(p.w_rows * nblk * SB));
+      make_rsrc(kFold ? static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk_r * SB : nullptr,
+                static_cast<uint32_t>(p.w_rows * nblk_r * SB));
   const __amdgpu_buffer_rsrc_t rs_sl =
-      make_rsrc(kFold ? static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk * SB : nullptr,
-                static_cast<uint32_t>(p.wl_rows * nblk * SB));
+      make_rsrc(kFold ? static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk_r * SB : nullptr,
+                static_cast<uint32_t>(p.wl_rows * nblk_r * SB));
   // this lane loads the scale row of block j = h, row lr
-  const uint32_t srow_off = static_cast<uint32_t>((row0 + drow[h]) * nblk * SB);
+  const int64_t srow = stiled ? wrow0 + wdrow[h] : row0 + drow[h];
+  const uint32_t srow_off = stiled ? static_cast<uint32_t>(((srow / 16) * 16 * nblk_r + (srow % 16) * nbc) * SB)
+                                   : static_cast<uint32_t>(srow * nblk * SB);
   const bool s_aligned = (nblk * SB) % 16 == 0;
+  // tile-major: dwords per chunk piece (log2: 0, 1 or 2) and bytes per chunk
+  const int s_per_log = stiled ? __builtin_ctz(static_cast<unsigned>(nbc * SB / 4)) : 0;
+  const uint32_t s_cstride = static_cast<uint32_t>(16 * nbc * SB);
   u32x4_t swin = {0u, 0u, 0u, 0u};  // window in flight (registers)
   auto sfetch = [&](int m) {        // window m: blocks [WB m, WB m + WB)
     if constexpr (kFold) {
+      if (stiled) {
+        // dword q of the window: piece q >> s_per_log (chunk WB m / nbc + that), dword q % per in it
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t o = srow_off + static_cast<uint32_t>(WB * m / nbc + (q >> s_per_log)) * s_cstride +
+                             4u * static_cast<uint32_t>(q & ((1 << s_per_log) - 1));
+          const uint32_t og = h == 0 ? o : kOob, ol = h == 1 ? o : kOob;
+          swin[q] = __builtin_amdgcn_raw_buffer_load_b32(rs_sg, static_cast<int>(og), 0, 0) |
+                    __builtin_amdgcn_raw_buffer_load_b32(rs_sl, static_cast<int>(ol), 0, 0);
+        }
+        return;
+      }
       const uint32_t o = srow_off + static_cast<uint32_t>(m * 16);
       const uint32_t og = h == 0 ? o : kOob, ol = h == 1 ? o : kOob;
       if (s_aligned) {
@@ -255,7 +290,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
       const __amdgpu_buffer_rsrc_t rw = GATED && j == 1 ? rs_l : rs_g;
-      const int sw = static_cast<int>(drow[j] * rb);
+      const int sw = static_cast<int>(wdrow[j] * rb);
 #pragma unroll
       for (int v = 0; v < BVEC; ++v)
         d.w[j][v] = __builtin_bit_cast(
@@ -615,6 +650,8 @@ hipError_t launch_fc1_prefill(const ExpertArgs& a, hipStream_t stream) {
   st.out_rows = a.T * a.k;
   st.out = a.act;
   st.tiled = a.tiled1;
+  st.deint = a.deint1;
+  st.stiled = a.stiled1;
   // gated: a weight tile holds BN/2 features (gate + linear rows)
   plan_grid(st, a.T, a.k, a.E, a.wfmt, gated ? 2 * a.I : a.I, 1);
   return launch_stage<true>(st, a, gated, stream);
@@ -646,6 +683,7 @@ hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half,
   st.out_rows = a.T * a.k;
   st.out = a.y2;
   st.tiled = a.tiled2;
+  st.stiled = a.stiled2;
   const int32_t splits = prefill_fc2_splits(a.T, a.H, a.I, a.E, a.k, a.wfmt);
   plan_grid(st, a.T, a.k, a.E, a.wfmt, a.H, splits);
   // fp16 and one plane: y2 goes out in fp16 (one rounding of the expert

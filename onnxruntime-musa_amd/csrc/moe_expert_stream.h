@@ -146,6 +146,31 @@ __device__ __forceinline__ u32x4_t dq4_f16_split(uint32_t v, uint32_t m_lo, uint
   return u32x4_t{(v & m_lo) | c, (v & m_hi) | c, (h & m_lo) | c, (h & m_hi) | c};
 }
 
+// 4 x 4 transpose of dwords across the four 16-lane rows of a wave (gfx950
+// row swaps): on entry v[j] of row r holds m[r][j]; on exit v[j] of row r
+// holds m[j][r].
+__device__ __forceinline__ void transpose_rows4(uint32_t* v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);  // [m00 m10 m02 m12], [m20 m30 m22 m32]
+  const auto b = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);  // [m01 m11 m03 m13], [m21 m31 m23 m33]
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  v[0] = c[0];
+  v[1] = c[1];
+  v[2] = d[0];
+  v[3] = d[1];
+}
+
+// o[r] = v of row r (same lane within the row), in every lane.
+__device__ __forceinline__ void gather_rows4(uint32_t v, uint32_t* o) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);        // [v0 v1 v0 v1], [v2 v3 v2 v3]
+  const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);  // [v0 x4], [v1 x4]
+  const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);  // [v2 x4], [v3 x4]
+  o[0] = b[0];
+  o[1] = b[1];
+  o[2] = c[0];
+  o[3] = c[1];
+}
+
 // K slices of the stream kernel: as few as fit the LDS slice, each a whole
 // number of ring blocks (pd chunks).  Equal slices without padding are
 // preferred (e.g. 112 chunks: 7 x 16 rather than 4 x 32 with the last half
@@ -173,8 +198,9 @@ inline int32_t stream_groups(int64_t T, int64_t E, int64_t k) {
 // entries; route_ints: routing results kept in LDS, 0 when the router
 // kernels route).  The routing scratch of the prologue overlays the slice.
 inline size_t stream_region_bytes(int ksc, int nw) {
+  // activation slice + bias sums per (32 k, row)
   const size_t act = static_cast<size_t>(kStreamRows) * (static_cast<size_t>(ksc) * 256 + 16) +
-                     static_cast<size_t>(ksc) * kStreamRows * 4;
+                     static_cast<size_t>(ksc) * 4 * kStreamRows * 4;
   const size_t slots = static_cast<size_t>(nw) * 2 * 64 * 16;
   return std::max(act, slots);
 }
@@ -185,17 +211,29 @@ inline size_t stream_lds_bytes(int ksc, int ngroups, int nw, int route_ints) {
 
 // NSC: folded scales (block 16/32/64): elements per lane and chunk (2 for
 // block 16); block scales: 4 = one load brings the scales of 4 chunks
-// (block 128, K a multiple of 512), 1 = one load per chunk.
+// (block 128, K a multiple of 512), 1 = one load per chunk; step scales:
+// 1 (lane group g loads the scale of step g's block).
 // STREAM_NT: the weights are tile-major (pre-packed), streamed with the
 // non-temporal cache policy.
+//
+// k assignment.  Loads are chunk-major: lane group g owns k [32 g, 32 g +
+// 32) of the chunk (one 16-byte piece of int4 per row), and, in every mode
+// but step, feeds 8 of them to each MFMA step, so a step's 32 k span the
+// chunk's four 32-k blocks.  Step-major (kScaleStep): step st takes k
+// [32 st, 32 st + 32), lane group g its 8 k at 32 st + 8 g, so a step lies
+// in one block of 32; the lanes of one row exchange their dwords with a 4 x
+// 4 transpose across lane groups (4 row swaps per 16 bytes), and the
+// activation slice is read at 64 st + 16 g.
 template <typename AT, int WF, int SM, typename ST, int NSC, bool FC1, bool GATED, bool STREAM_NT>
 __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_kernel(StreamStage ss) {
   using G = SGeo<WF, GATED>;
   constexpr int kAux = STREAM_NT ? kStreamAux : 0;
   constexpr int NW = G::NW, NT = NW * 64, WT = G::WT, FT = G::FT, PD = G::PD, LB = G::kLaneBytes;
-  constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan);
+  constexpr bool kStep = SM == kScaleStep;
+  constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan || kStep);
+  static_assert(!kStep || (Biased<AT, WF>::kOk && NSC == 1), "step scales: biased operands, one scale per lane");
   constexpr bool kSplit = kBiased && WF == kInt4 && AT::kId == 10;
-  constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold;
+  constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold || kStep;
   constexpr bool kGroupScales = SM == kScaleBlock && NSC == 4;
   // 2-byte block scales of block 128 are loaded per tile: one load per
   // lane (row col, lane group g) brings the 16 bytes that hold the scales
@@ -225,7 +263,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   int* lroute = reinterpret_cast<int*>(smem + (ss.ngroups * 4 + 15) / 16 * 16);  // [E + 1] offsets, [T k] perm
   uint8_t* region = smem + (ss.ngroups * 4 + 15) / 16 * 16 + (ss.route_ints * 4 + 15) / 16 * 16;
   uint8_t* xs = region;                                         // [16][pitch] activation slice
-  float* corr = reinterpret_cast<float*>(region + 16 * pitch);  // [ksc][16] bias sums per chunk and row
+  // bias sums per row: [ksc][16] per chunk, step scales [ksc * 4][16] per 32 k
+  float* corr = reinterpret_cast<float*>(region + 16 * pitch);
   float* slots = reinterpret_cast<float*>(region);              // [NW][WT][64] float4, after the compute
 
   // ---- routing (fc1 of a small batch): every workgroup computes the same
@@ -275,8 +314,12 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   const int64_t K = p.K;
   const int nchunks = static_cast<int>((K + kChunk - 1) / kChunk);
   const int ktail = static_cast<int>(K - static_cast<int64_t>(nchunks - 1) * kChunk);
-  const uint32_t rb = static_cast<uint32_t>((K / 32) * LB);  // bytes of one weight row
-  const int nft = static_cast<int>((p.nfeat + 16 * FT - 1) / (16 * FT));
+  // Tile-major weights (pre-packed) hold whole chunks: a row's K is padded
+  // with zeros to nchunks * 128 k.
+  const bool tiled = STREAM_NT || p.tiled != 0;
+  const uint32_t rb = tiled ? static_cast<uint32_t>(nchunks * 4 * LB)
+                            : static_cast<uint32_t>((K / 32) * LB);  // bytes of one weight row
+  const int nft =static_cast<int>((p.nfeat + 16 * FT - 1) / (16 * FT));
   // tile counts stay far below 2^31 (row groups x slices x feature tiles),
   // so the partition and the group loop use 32-bit arithmetic
   const int per_a = nsl * nft;
@@ -318,13 +361,24 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // chunked).  Lane constants: feature offset fo[u] inside a tile, and the
   // row's byte offsets with the tile index factored out (32-bit: one
   // expert's weights are below 2 GiB).
+  // Scales and biases of the interleaved layout: rows 2f / 2f + 1.  The
+  // weights too, unless pre-packed de-interleaved (gate f, linear nfeat + f).
   const int rmul = (FC1 && GATED && p.gate_mode == kGateInterleaved) ? 2 : 1;
+  const bool deint = FC1 && GATED && tiled && p.deint != 0;
+  const int wmul = deint ? 1 : rmul;
+  // Tile-major step scales (pre-packed): per (16-row tile, chunk) the 16
+  // rows' nbc = 128 / block scales, 16 * nbc contiguous elements (rows as
+  // the weights'); nblk_r: their elements per row, with K padded to whole
+  // chunks.  One load instruction then reads 16 * nbc * 2 (or 4) bytes in
+  // one run instead of one cache line per row.
+  const bool stiled = kStep && tiled && p.stiled != 0;
+  const int nbc = kChunk >> bshift;
+  const uint32_t nblk_r = stiled ? static_cast<uint32_t>(nchunks * nbc) : nblk;
   // Tile-major weights (pre-packed; weight tiles start at a multiple of 16
   // rows, K is whole chunks): the 16 rows x 128 k of a weight tile and chunk
   // are one contiguous block, lane l's 16 bytes at 16 l (vector v of int8
   // one 1 KB block further), so that each load instruction reads 1 KB in
   // one run.  Row-major: row col, bytes [LB g, LB g + LB) of the chunk.
-  const bool tiled = STREAM_NT || p.tiled != 0;
   const uint32_t cstride = tiled ? 64 * LB : 4 * LB;  // weight bytes per chunk
   const int vdelta = tiled ? 1024 - 16 : 0;           // extra offset of vector v, per v
   int fo[WT], rowb[WT];
@@ -335,11 +389,15 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     const int radd = !lin ? 0 : (p.gate_mode == kGateInterleaved ? 1 : (p.gate_mode == kGateChunked ? nfeat : 0));
     fo[u] = (u % FT) * 16 + col;
     rowb[u] = fo[u] * rmul + radd;
-    wb[u] = tiled ? static_cast<uint32_t>(rowb[u] - col) * rb + lane * 16 : static_cast<uint32_t>(rowb[u]) * rb + g * LB;
-    sb[u] = static_cast<uint32_t>(rowb[u]) * nblk * kEs;
+    const int wrow = deint ? fo[u] + (lin ? nfeat : 0) : rowb[u];
+    wb[u] = tiled ? static_cast<uint32_t>(wrow - col) * rb + lane * 16 : static_cast<uint32_t>(wrow) * rb + g * LB;
+    // tile-major scales: lane (col, g) reads scale (32 g) / block of row col
+    sb[u] = stiled ? (static_cast<uint32_t>(wrow - col) * nblk_r + static_cast<uint32_t>(col * nbc + ((32 * g) >> bshift))) * kEs
+                   : static_cast<uint32_t>(rowb[u]) * nblk * kEs;
   }
-  const uint32_t tws = static_cast<uint32_t>(16 * FT * rmul) * rb;          // weight bytes per tile step
-  const uint32_t tss = static_cast<uint32_t>(16 * FT * rmul) * nblk * kEs;  // scale bytes per tile step
+  const uint32_t tws = static_cast<uint32_t>(16 * FT * wmul) * rb;          // weight bytes per tile step
+  const uint32_t tss = stiled ? static_cast<uint32_t>(16 * FT * wmul) * nblk_r * kEs
+                              : static_cast<uint32_t>(16 * FT * rmul) * nblk * kEs;  // scale bytes per tile step
   // masks of the int4 nibble split, kept in VGPRs so that each output pair
   // is one v_and_or_b32
   uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
@@ -368,10 +426,10 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
                                                   static_cast<uint32_t>(p.wl_rows * rb));
     __amdgpu_buffer_rsrc_t ss_g = rs_g, ss_l = rs_l;
     if constexpr (kRingScales) {
-      ss_g = make_rsrc(static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk * kEs,
-                       static_cast<uint32_t>(p.w_rows * nblk * kEs));
-      ss_l = make_rsrc(static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk * kEs,
-                       static_cast<uint32_t>(p.wl_rows * nblk * kEs));
+      ss_g = make_rsrc(static_cast<const uint8_t*>(p.s) + static_cast<int64_t>(e) * p.w_rows * nblk_r * kEs,
+                       static_cast<uint32_t>(p.w_rows * nblk_r * kEs));
+      ss_l = make_rsrc(static_cast<const uint8_t*>(p.sl) + static_cast<int64_t>(e) * p.wl_rows * nblk_r * kEs,
+                       static_cast<uint32_t>(p.wl_rows * nblk_r * kEs));
     }
 
     // weight / scale offsets of tile tl (relative to the group) for this lane
@@ -405,8 +463,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
       // padding chunks past K and the missing lanes of a partial last chunk
       // read nothing (branch-free: one compare against the chunk's valid k)
       const int kval = cg < nchunks - 1 ? kChunk : (cg == nchunks - 1 ? ktail : 0);
-      const uint32_t oob = 32 * g + 32 <= kval ? 0u : kOob;
       const uint32_t wc = static_cast<uint32_t>(cg) * cstride;
+      const uint32_t oob = 32 * g + 32 <= kval ? 0u : kOob;
 #pragma unroll
       for (int u = 0; u < WT; ++u) {
         const uint32_t o = (woff[u] + wc) | oob;
@@ -416,10 +474,13 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
                                                       GATED && u >= FT ? rs_l : rs_g, static_cast<int>(o + 16 * v),
                                                       v * vdelta, kAux));
         if constexpr (kRingScales && !kTileScales) {
-          const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (SM == kScaleFold ? 32 * g : 0);
+          // folded and step scales: the block of lane group g's 32 k
+          constexpr bool kPerGroup = SM == kScaleFold || kStep;
+          const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (kPerGroup ? 32 * g : 0);
           // a block scale multiplies the whole chunk's sum (every lane group
           // of the MFMA output), so only a chunk past K reads none
-          const uint32_t so = (soff[u] + (kk >> bshift) * kEs) | (SM == kScaleFold ? oob : (cg < nchunks ? 0u : kOob));
+          const uint32_t so = stiled ? (soff[u] + static_cast<uint32_t>(cg * 16 * nbc * kEs)) | oob
+                                     : (soff[u] + (kk >> bshift) * kEs) | (kPerGroup ? oob : (cg < nchunks ? 0u : kOob));
           // grouped: the first chunk of each group of 4 loads all 4 scales
           if (!kGroupScales || (cl & 3) == 0) d.sc[u] = SR::template load<kAux>(GATED && u >= FT ? ss_l : ss_g, so);
         }
@@ -472,7 +533,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     // Each wave finishes the pieces it loaded: the int4 split (odd k / 16
     // and the k order of the weights) in place, and the bias sums per
     // (chunk, row) of biased operands (the 16 pieces of one (row, chunk) sit
-    // in 16 consecutive lanes).
+    // in 16 consecutive lanes; step-major: per (32 k, row), 4 lanes).
     if constexpr (kBiased) {
       for (int q = wave; q < ngr; q += NW) {
         const int m = q / gpr, r = (q - m * gpr) * 64 + lane;
@@ -509,9 +570,11 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           }
           cs = Biased<AT, WF>::kOffset * sum;
         }
+        // per chunk (16 pieces) or, step-major, per 32 k (4 pieces)
+        constexpr int kSumPieces = kStep ? 4 : 16;
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) cs += __shfl_xor(cs, o, kWave);
-        if ((r & 15) == 0) corr[(r >> 4) * kStreamRows + m] = cs;
+        for (int o = 1; o < kSumPieces; o <<= 1) cs += __shfl_xor(cs, o, kWave);
+        if ((r & (kSumPieces - 1)) == 0) corr[(r / kSumPieces) * kStreamRows + m] = cs;
       }
     }
     __syncthreads();
@@ -534,6 +597,60 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     u32x2_t bsc[WT];
     auto compute = [&](int cl, int slot) {
       const CK& d = ring[slot];
+      if constexpr (kStep) {
+        // Step st: k [32 st, 32 st + 32) of the chunk, one scale block.  The
+        // result is sum_st s_st * (mfma_st - c_st): the products s_st * mfma_st
+        // go to acc with one fma per element, and the bias sums c_st (per
+        // row) times the scales (per feature) are one 16 x 16 x 4 fp32 MFMA
+        // per chunk with A[row][st] = -c_st[row], B[st][feature] = s_st: lane
+        // (col, g) holds A[col][g] and its own block scale B[g][col].
+        const uint8_t* xr = xs + col * pitch + cl * 256 + g * 16;
+        const floatx4_t zero = {0.f, 0.f, 0.f, 0.f};
+        const float ncr = -corr[(cl * 4 + g) * kStreamRows + col];
+        u32x4_t wq[WT][G::kVecs];
+        float s4[WT][4];
+#pragma unroll
+        for (int u = 0; u < WT; ++u) {
+          if constexpr (WF == kInt4) {
+            uint32_t v[4] = {d.w[u][0][0], d.w[u][0][1], d.w[u][0][2], d.w[u][0][3]};
+            transpose_rows4(v);
+            wq[u][0] = u32x4_t{v[0], v[1], v[2], v[3]};
+          } else {
+            // 8 k = two dwords per step: transpose the even and the odd ones
+            uint32_t ev[4], od[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              ev[j] = d.w[u][j >> 1][(j & 1) * 2];
+              od[j] = d.w[u][j >> 1][(j & 1) * 2 + 1];
+            }
+            transpose_rows4(ev);
+            transpose_rows4(od);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              wq[u][j >> 1][(j & 1) * 2] = ev[j];
+              wq[u][j >> 1][(j & 1) * 2 + 1] = od[j];
+            }
+          }
+          const float sg = SR::elem(d.sc[u], 0);
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(ncr, sg, acc[u], 0, 0, 0);
+          uint32_t g4[4];
+          gather_rows4(__float_as_uint(sg), g4);
+#pragma unroll
+          for (int st = 0; st < 4; ++st) s4[u][st] = __uint_as_float(g4[st]);
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xr + 64 * st);
+#pragma unroll
+          for (int u = 0; u < WT; ++u) {
+            u32x4_t bw;
+            if constexpr (kSplit) bw = dq4_f16_split(wq[u][0][st], m_lo, m_hi);
+            else bw = weight_biased<AT, WF>(wq[u], st);
+            acc[u] += mfma16x16x32<AT>(av, bw, zero) * s4[u][st];
+          }
+        }
+        return;
+      }
       floatx4_t tmp[WT];
 #pragma unroll
       for (int u = 0; u < WT; ++u) tmp[u] = floatx4_t{0.f, 0.f, 0.f, 0.f};
@@ -812,6 +929,16 @@ hipError_t launch_stream_fmt(const StreamStage& ss, const ExpertArgs& a, bool fc
       // block 128 and K a multiple of 512: 4 chunks' scales are one aligned load
       if (a.block_size == 128 && ss.s.K % 512 == 0) return bf ? by_st(BF16{}, BLK{}, FOUR{}) : by_st(F16{}, BLK{}, FOUR{});
       return bf ? by_st(BF16{}, BLK{}, ONE{}) : by_st(F16{}, BLK{}, ONE{});
+    }
+    // blocks of 32 / 64 with a biased operand form: step scales
+    using STEP = std::integral_constant<int, kScaleStep>;
+    if (a.block_size == 32 || a.block_size == 64) {
+      if constexpr (WF == kInt4) {
+        return bf ? by_st(BF16{}, STEP{}, ONE{}) : by_st(F16{}, STEP{}, ONE{});
+      } else {
+        // int8: biased operands with fp16 activations only
+        if (!bf) return by_st(F16{}, STEP{}, ONE{});
+      }
     }
     // folded block scales: a lane's 32 k span two blocks of 16
     if (a.block_size == 16) return bf ? by_st(BF16{}, FOLD{}, TWO{}) : by_st(F16{}, FOLD{}, TWO{});

@@ -80,6 +80,10 @@ struct ExpertArgs {
   // 1: the stage's weights are in the tile-major layout of moe_prepack.hip
   // (fc1 and fc3 together; fc2), else in the op's row-major layout
   int32_t tiled1, tiled2;
+  // 1: the tile-major fused fc1 of interleaved SwiGLU is de-interleaved
+  int32_t deint1;
+  // 1: the stage's block scales (block 32 / 64) are tile-major too
+  int32_t stiled1, stiled2;
   // intermediates
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
@@ -116,11 +120,21 @@ hipError_t launch_softmax(const void* in, void* out, int32_t elem_type, int64_t 
                           hipStream_t stream);
 
 // Reorders row-major quantized weights [rows, row_bytes] (rows a multiple of
-// 16, row_bytes a multiple of the chunk row bytes cbytes = 64 for int4, 128
-// for int8) into the tile-major layout read by the decode and prefill kernels
-// (moe_prepack.hip).
+// 16 and of expert_rows, row_bytes a multiple of 16) into the tile-major
+// layout read by the decode and prefill kernels (moe_prepack.hip): rows of
+// ceil(row_bytes / cbytes) * cbytes bytes (cbytes = 64 for int4, 128 for
+// int8; the padding is zeros), with each expert's interleaved row pairs
+// split into halves when deint (expert_rows a multiple of 32).
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
-                          hipStream_t stream);
+                          int64_t expert_rows, bool deint, hipStream_t stream);
+// Reorders block scales [rows, nblk] of block 32 or 64 (elem_bytes 2 or 4)
+// into the tile-major layout of the step-scale decode kernels: per (16-row
+// tile, chunk of 128 k) the 16 rows' 128 / block scales, blocks past K zero,
+// rows de-interleaved like their weights when deint (moe_prepack.hip).
+hipError_t launch_prepack_scales(const void* src, void* dst, int elem_bytes, int64_t rows, int64_t nblk, int block,
+                                 int64_t expert_rows, bool deint, hipStream_t stream);
+// Bytes of one packed weight row: K padded to whole chunks of 128.
+inline int64_t packed_row_bytes(int64_t K, int wfmt) { return (K + 127) / 128 * (wfmt == kInt4 ? 64 : 128); }
 
 // Whether the MFMA paths accept this problem (fp16/bf16 activations, K a
 // multiple of 32, block sizes the dequant loaders handle).

@@ -129,6 +129,7 @@ struct moe_kernel {
   struct Packed {
     const void* data = nullptr;
     moe_tensor src{};
+    bool deint = false;  // fused interleaved fc1 stored de-interleaved
   };
   Packed packed[11];
 
@@ -315,19 +316,52 @@ bool env_set(const char* name) {
 
 // Bytes of the tile-major copy of QMoE weight input idx, or 0 when the
 // kernels read that input in the op's layout (see moe_prepack.hip).  A
-// weight is packed when each expert's rows are whole 16-row tiles and K is
-// whole chunks of 128, and the kernels that read it take tile-major weights:
-// fp16/bf16 activations (MFMA paths); fc1/fc3 with K within one decode
-// activation slice and gate/linear rows in separate tiles (not interleaved).
+// weight is packed when each expert's rows are whole 16-row tiles (the
+// gate and linear halves of a fused fc1 each), rows are whole 16-byte
+// pieces (K is padded to whole chunks of 128 in the copy), and the kernels
+// that read it take tile-major weights: fp16/bf16 activations (MFMA paths);
+// fc1/fc3 with K within one decode activation slice.
+// Bytes of the tile-major copy of QMoE block-scale input idx (3 fc1, 6
+// fc2, 9 fc3), or 0: scales are packed for the step-scale decode kernels
+// (block 32 or 64; int4, or int8 with fp16 activations) when their weights
+// are packed too (same row and K rules).
+size_t prepack_scale_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* s, int32_t act_type) {
+  const moe_attributes& at = kr->attrs;
+  const int64_t bs = at.block_size;
+  if (bs != 32 && bs != 64) return 0;
+  if (act_type != MOE_ELEM_FLOAT16 && act_type != MOE_ELEM_BFLOAT16) return 0;
+  if (at.expert_weight_bits == 8 && act_type != MOE_ELEM_FLOAT16) return 0;
+  const int64_t E = s->dims[0], N = s->dims[1], nblk = s->dims[2];
+  const int64_t es = s->elem_type == MOE_ELEM_FLOAT ? 4 : 2;
+  if (N <= 0 || N % 16 || nblk <= 0) return 0;
+  const int64_t nchunks = (nblk * bs + 127) / 128;
+  const int64_t cbytes = at.expert_weight_bits == 4 ? 64 : 128;
+  if (N * nchunks * cbytes >= (int64_t{1} << 31)) return 0;  // the weights' packing rule
+  const bool swiglu = at.activation_type == MOE_ACT_SWIGLU;
+  if (idx != 6) {
+    if (nchunks * 128 > moe::kStreamMaxK) return 0;
+    if (swiglu && (at.swiglu_fusion == 1 || at.swiglu_fusion == 2) && N % 32) return 0;
+  }
+  return static_cast<size_t>(E * N * nchunks * (128 / bs) * es);
+}
+
 moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w, int32_t act_type,
                          size_t* bytes) {
   *bytes = 0;
-  if (idx != 2 && idx != 5 && idx != 8)
-    return fail(MOE_INVALID_ARGUMENT, "input_index must be 2, 5 or 8 (QMoE expert weights), got " +
-                                          std::to_string(idx));
+  const bool scales = idx == 3 || idx == 6 || idx == 9;
+  if (idx != 2 && idx != 5 && idx != 8 && !scales)
+    return fail(MOE_INVALID_ARGUMENT, "input_index must be 2, 5 or 8 (QMoE expert weights) or 3, 6 or 9 "
+                                      "(their scales), got " + std::to_string(idx));
   if (!w || !w->data) return fail(MOE_INVALID_ARGUMENT, "null weights");
   if (!is_float_type(act_type)) return fail(MOE_INVALID_ARGUMENT, "act_type must be a float type");
   if (!kr->quantized) return MOE_OK;
+  if (scales) {
+    // per output channel [E, N] (kept as given) or per block [E, N, K / block]
+    if ((w->rank != 2 && w->rank != 3) || !is_float_type(w->elem_type) || w->dims[0] <= 0)
+      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must be 2D or 3D float, got " + dims_str(*w));
+    if (w->rank == 3) *bytes = prepack_scale_bytes(kr, idx, w, act_type);
+    return MOE_OK;
+  }
   if (w->elem_type != MOE_ELEM_UINT8 || w->rank != 3 || w->dims[0] <= 0)
     return fail(MOE_INVALID_ARGUMENT, "QMoE expert weights must be 3D uint8, got " + dims_str(*w));
   if (act_type == MOE_ELEM_FLOAT) return MOE_OK;
@@ -335,15 +369,21 @@ moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w,
   const int64_t cbytes = at.expert_weight_bits == 4 ? 64 : 128;
   const int64_t E = w->dims[0], N = w->dims[1], rb = w->dims[2];
   const bool swiglu = at.activation_type == MOE_ACT_SWIGLU;
-  if (N <= 0 || N % 16 || rb <= 0 || rb % cbytes) return MOE_OK;
-  if (N * rb >= (int64_t{1} << 31)) return MOE_OK;  // 32-bit buffer offsets per expert
+  if (N <= 0 || N % 16 || rb <= 0 || rb % 16) return MOE_OK;
+  const int64_t rbp = (rb + cbytes - 1) / cbytes * cbytes;  // padded to whole chunks
+  if (N * rbp >= (int64_t{1} << 31)) return MOE_OK;        // 32-bit buffer offsets per expert
   if (idx != 5) {
-    if (rb / cbytes * 128 > moe::kStreamMaxK) return MOE_OK;
-    if (swiglu && at.swiglu_fusion == 1) return MOE_OK;
-    if (swiglu && at.swiglu_fusion == 2 && N % 32) return MOE_OK;
+    if (rbp / cbytes * 128 > moe::kStreamMaxK) return MOE_OK;
+    if (swiglu && (at.swiglu_fusion == 1 || at.swiglu_fusion == 2) && N % 32) return MOE_OK;
   }
-  *bytes = static_cast<size_t>(E * N * rb);
+  *bytes = static_cast<size_t>(E * N * rbp);
   return MOE_OK;
+}
+
+// Whether input idx is packed de-interleaved: the fused fc1 of interleaved
+// SwiGLU (weights and scales).
+bool prepack_deint(const moe_kernel* kr, int32_t idx) {
+  return (idx == 2 || idx == 3) && kr->attrs.activation_type == MOE_ACT_SWIGLU && kr->attrs.swiglu_fusion == 1;
 }
 
 moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout& l, uint8_t* ws,
@@ -377,6 +417,9 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   }
   a.tiled1 = q && kr->packed[2].data ? 1 : 0;
   a.tiled2 = q && kr->packed[5].data ? 1 : 0;
+  a.deint1 = a.tiled1 && kr->packed[2].deint ? 1 : 0;
+  a.stiled1 = q && kr->packed[3].data ? 1 : 0;
+  a.stiled2 = q && kr->packed[6].data ? 1 : 0;
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
   a.y2_planes = 1;
@@ -509,12 +552,20 @@ moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe
     if (reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(weights->data) % 16)
       return fail(MOE_INVALID_ARGUMENT, "weights and pre-pack buffer must be 16-byte aligned");
     const int cbytes = kernel->attrs.expert_weight_bits == 4 ? 64 : 128;
-    const hipError_t e = moe::launch_prepack(static_cast<const uint8_t*>(weights->data), static_cast<uint8_t*>(dst),
-                                             weights->dims[0] * weights->dims[1], weights->dims[2], cbytes,
-                                             static_cast<hipStream_t>(stream));
+    const bool deint = prepack_deint(kernel, input_index);
+    const bool scales = input_index == 3 || input_index == 6 || input_index == 9;
+    const hipError_t e =
+        scales ? moe::launch_prepack_scales(weights->data, dst, weights->elem_type == MOE_ELEM_FLOAT ? 4 : 2,
+                                            weights->dims[0] * weights->dims[1], weights->dims[2],
+                                            static_cast<int>(kernel->attrs.block_size), weights->dims[1], deint,
+                                            static_cast<hipStream_t>(stream))
+               : moe::launch_prepack(static_cast<const uint8_t*>(weights->data), static_cast<uint8_t*>(dst),
+                                     weights->dims[0] * weights->dims[1], weights->dims[2], cbytes, weights->dims[1],
+                                     deint, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pre-pack launch");
     kernel->packed[input_index].data = dst;
     kernel->packed[input_index].src = *weights;
+    kernel->packed[input_index].deint = deint;
     *is_packed = 1;
     return MOE_OK;
   } catch (const std::exception& e) {
@@ -669,8 +720,11 @@ moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int3
       ra.hidden = p.H;
     }
     moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
-    if (p.gate_mode == moe::kGateFc3 && (kernel->packed[2].data != nullptr) != (kernel->packed[8].data != nullptr))
-      return fail(MOE_NOT_IMPLEMENTED, "fc1 and fc3 weights must both be pre-packed or neither");
+    auto packed = [&](int i) { return kernel->packed[i].data != nullptr; };
+    if (p.gate_mode == moe::kGateFc3 && (packed(2) != packed(8) || packed(3) != packed(9)))
+      return fail(MOE_NOT_IMPLEMENTED, "fc1 and fc3 weights (and scales) must both be pre-packed or neither");
+    if ((packed(3) && !packed(2)) || (packed(6) && !packed(5)) || (packed(9) && !packed(8)))
+      return fail(MOE_NOT_IMPLEMENTED, "pre-packed scales need their weights pre-packed");
     const int path = choose_path(kernel, a);
     if (path < 0)
       return fail(MOE_NOT_IMPLEMENTED, kernel->forced_path >= 0

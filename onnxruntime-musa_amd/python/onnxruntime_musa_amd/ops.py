@@ -266,7 +266,9 @@ class QMoE(_MoEOp):
     """com.microsoft QMoE (int8 / int4 expert weights with scales)."""
     op_type = "QMoE"
     input_names = QMOE_INPUTS
-    WEIGHT_INPUTS = (2, 5, 8)  # fc1, fc2, fc3 expert weights
+    # fc1, fc2, fc3 expert weights and their block scales (packed for the
+    # step-scale decode kernels: block 32 / 64)
+    WEIGHT_INPUTS = (2, 3, 5, 6, 8, 9)
 
 
 def route_dispatch(logits: torch.Tensor, k: int, normalize: bool = False, sigmoid: bool = False,

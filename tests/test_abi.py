@@ -278,33 +278,61 @@ def prepack_size(lib, h, idx, dims, act=C.ELEM_FLOAT16, et=C.ELEM_UINT8):
     return st, n.value
 
 
-@pytest.mark.parametrize("bits,idx,dims,packed", [
-    (4, 2, [8, 512, 128], True),     # fc1 int4: H = 256 -> whole chunks, 16-row tiles
-    (4, 5, [8, 256, 256], True),     # fc2 int4, I = 512
-    (4, 8, [8, 512, 128], True),     # fc3
-    (8, 2, [8, 512, 256], True),     # int8
-    (4, 2, [8, 520, 128], False),    # N not a multiple of 16
-    (4, 2, [8, 512, 96], False),     # K = 192: not whole chunks of 128
-    (8, 5, [8, 256, 192], False),    # int8 K = 192
-    (4, 2, [8, 512, 4096], False),   # fc1 K = 8192: above one decode activation slice
-    (4, 5, [8, 512, 4096], True),    # fc2 K = 8192 streams in slices
+# packed row bytes: K padded to whole chunks of 128 (64 bytes int4, 128 int8)
+@pytest.mark.parametrize("bits,idx,dims,packed_rb", [
+    (4, 2, [8, 512, 128], 128),      # fc1 int4: H = 256 -> whole chunks, 16-row tiles
+    (4, 5, [8, 256, 256], 256),      # fc2 int4, I = 512
+    (4, 8, [8, 512, 128], 128),      # fc3
+    (8, 2, [8, 512, 256], 256),      # int8
+    (4, 2, [8, 520, 128], 0),        # N not a multiple of 16
+    (4, 2, [8, 512, 96], 128),       # K = 192: padded to 2 chunks
+    (8, 5, [8, 256, 192], 256),      # int8 K = 192
+    (4, 5, [8, 2880, 1440], 1472),   # gpt-oss fc2 K = 2880: 22.5 chunks -> 23
+    (4, 2, [8, 512, 100], 0),        # rows not whole 16-byte pieces
+    (4, 2, [8, 512, 4096], 0),       # fc1 K = 8192: above one decode activation slice
+    (4, 5, [8, 512, 4096], 4096),    # fc2 K = 8192 streams in slices
 ])
-def test_prepack_size_rules(lib, bits, idx, dims, packed):
+def test_prepack_size_rules(lib, bits, idx, dims, packed_rb):
     st, h = create(lib, "QMoE", k=2, activation_type=4, block_size=128, expert_weight_bits=bits)
     assert st == C.MOE_OK
     try:
         st, n = prepack_size(lib, h, idx, dims)
         assert st == C.MOE_OK, lib.moe_last_error()
-        assert n == (dims[0] * dims[1] * dims[2] if packed else 0)
+        assert n == dims[0] * dims[1] * packed_rb
     finally:
         lib.moe_kernel_release(h)
 
 
-def test_prepack_size_interleaved_fc1_stays_row_major(lib):
+@pytest.mark.parametrize("bits,block,act,idx,dims,elem,packed", [
+    (4, 32, C.ELEM_BFLOAT16, 3, [8, 5760, 90], C.ELEM_BFLOAT16, 8 * 5760 * 23 * 4 * 2),  # gpt-oss fc1
+    (4, 32, C.ELEM_BFLOAT16, 6, [8, 2880, 90], C.ELEM_BFLOAT16, 8 * 2880 * 23 * 4 * 2),
+    (4, 64, C.ELEM_FLOAT16, 6, [8, 256, 5], C.ELEM_FLOAT, 8 * 256 * 3 * 2 * 4),          # K = 320: 3 chunks
+    (8, 32, C.ELEM_FLOAT16, 9, [8, 512, 8], C.ELEM_FLOAT16, 8 * 512 * 2 * 4 * 2),
+    (8, 32, C.ELEM_BFLOAT16, 3, [8, 512, 8], C.ELEM_BFLOAT16, 0),  # int8 + bf16: folded scales
+    (4, 128, C.ELEM_FLOAT16, 3, [8, 512, 2], C.ELEM_FLOAT16, 0),   # block 128: per-chunk scales
+    (4, 16, C.ELEM_FLOAT16, 3, [8, 512, 16], C.ELEM_FLOAT16, 0),   # block 16: folded
+    (4, 32, C.ELEM_FLOAT16, 3, [8, 520, 8], C.ELEM_FLOAT16, 0),    # N not a multiple of 16
+    (4, 32, C.ELEM_FLOAT16, 6, [8, 512], C.ELEM_FLOAT16, 0),       # per-channel scales stay as given
+])
+def test_prepack_size_scales(lib, bits, block, act, idx, dims, elem, packed):
+    st, h = create(lib, "QMoE", k=2, activation_type=4, swiglu_fusion=1, block_size=block,
+                   expert_weight_bits=bits)
+    assert st == C.MOE_OK
+    try:
+        assert prepack_size(lib, h, idx, dims, act=act, et=elem) == (C.MOE_OK, packed)
+    finally:
+        lib.moe_kernel_release(h)
+
+
+def test_prepack_size_interleaved_fc1(lib):
+    # the fused fc1 of interleaved SwiGLU is packed de-interleaved: each
+    # half (gate rows, linear rows) must be whole 16-row tiles
     st, h = create(lib, "QMoE", k=2, activation_type=4, swiglu_fusion=1, block_size=32)
     assert st == C.MOE_OK
     try:
-        assert prepack_size(lib, h, 2, [8, 1024, 128]) == (C.MOE_OK, 0)
+        assert prepack_size(lib, h, 2, [8, 1024, 128]) == (C.MOE_OK, 8 * 1024 * 128)
+        assert prepack_size(lib, h, 2, [8, 5760, 1440]) == (C.MOE_OK, 8 * 5760 * 1472)
+        assert prepack_size(lib, h, 2, [8, 1040, 128]) == (C.MOE_OK, 0)
         assert prepack_size(lib, h, 5, [8, 256, 256])[1] == 8 * 256 * 256
     finally:
         lib.moe_kernel_release(h)
@@ -331,7 +359,9 @@ def test_prepack_size_fp32_activations_and_moe_stay_row_major(lib, qkernel):
 
 
 @pytest.mark.parametrize("idx,dims,et,act", [
-    (3, [8, 512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),   # a scale input
+    (3, [8, 512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),   # scales that are not a float type
+    (6, [8, 512, 4, 1], C.ELEM_FLOAT16, C.ELEM_FLOAT16),  # scales neither 2D nor 3D
+    (4, [8, 512], C.ELEM_FLOAT16, C.ELEM_FLOAT16),       # a bias input
     (0, [16, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16),
     (2, [512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),      # not 3D
     (2, [8, 512, 128], C.ELEM_FLOAT16, C.ELEM_FLOAT16),  # not uint8
