@@ -33,13 +33,14 @@
 //
 // Biased operands: int8/int4 weights enter the MFMA with their zero point
 // and magic-exponent bias still in (1024 + q for fp16, 128 + q for bf16),
-// and the bias is removed per chunk (block scales) or once (per-channel
-// scales) with per-row activation sums computed while staging.  For int4
-// with fp16 activations, the nibbles are placed into the 16-bit lanes with
-// two and-or operations per pair: the odd nibbles land 4 bits up (1024 +
-// 16 q), so the activations at those k are staged divided by 16 (exact),
-// and the k order inside each 8-k step is (0 4 1 5 2 6 3 7) in both
-// operands.
+// and the bias is removed per chunk (block scales), per MFMA step (step
+// scales) or once (per-channel scales) with per-row activation sums
+// computed while staging.  For int4, the nibbles are placed into the 16-bit
+// lanes with one and-or operation per pair (fp16) or a shift and an and-or
+// (bf16, odd pairs): the odd nibbles land 4 bits up (1024 + 16 q) or 1 bit
+// down (128 + 8 q), so the activations at those k are staged divided by 16
+// or 8 (exact), and the k order inside each 8-k step is (0 4 1 5 2 6 3 7)
+// in both operands.
 //
 // fc1 needs the whole K in one slice (its activation needs the full sum);
 // fc2 writes one fp32 plane of y2 per K slice, which the finalize pass sums
@@ -146,6 +147,20 @@ __device__ __forceinline__ u32x4_t dq4_f16_split(uint32_t v, uint32_t m_lo, uint
   return u32x4_t{(v & m_lo) | c, (v & m_hi) | c, (h & m_lo) | c, (h & m_hi) | c};
 }
 
+// The bf16 form: 128 + q in the same k order, the odd-k pairs 128 + 8 q (a
+// bf16 of magnitude 128..255 has 7 mantissa bits, so an odd nibble moves 1
+// bit down, not 4 up).  m_lo = 0x000F000F, m_hi = 0x00780078.
+__device__ __forceinline__ u32x4_t dq4_bf16_split(uint32_t v, uint32_t m_lo, uint32_t m_hi) {
+  const uint32_t c = 0x43004300u, h = v >> 8;
+  return u32x4_t{(v & m_lo) | c, ((v >> 1) & m_hi) | c, (h & m_lo) | c, ((h >> 1) & m_hi) | c};
+}
+
+// Both halves of a bf16 pair times 1/8 (exact for normal values).
+__device__ __forceinline__ uint32_t bf16x2_eighth(uint32_t w) {
+  const float lo = __uint_as_float(w << 16) * 0.125f, hi = __uint_as_float(w & 0xFFFF0000u) * 0.125f;
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+
 // 4 x 4 transpose of dwords across the four 16-lane rows of a wave (gfx950
 // row swaps): on entry v[j] of row r holds m[r][j]; on exit v[j] of row r
 // holds m[j][r].
@@ -233,6 +248,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan || kStep);
   static_assert(!kStep || (Biased<AT, WF>::kOk && NSC == 1), "step scales: biased operands, one scale per lane");
   constexpr bool kSplit = kBiased && WF == kInt4 && AT::kId == 10;
+  constexpr bool kSplitB = kBiased && WF == kInt4 && AT::kId == 16;
   constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold || kStep;
   constexpr bool kGroupScales = SM == kScaleBlock && NSC == 4;
   // 2-byte block scales of block 128 are loaded per tile: one load per
@@ -400,8 +416,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
                               : static_cast<uint32_t>(16 * FT * rmul) * nblk * kEs;  // scale bytes per tile step
   // masks of the int4 nibble split, kept in VGPRs so that each output pair
   // is one v_and_or_b32
-  uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u;
-  if constexpr (kSplit) {
+  uint32_t m_lo = 0x000F000Fu, m_hi = kSplitB ? 0x00780078u : 0x00F000F0u;
+  if constexpr (kSplit || kSplitB) {
     asm volatile("" : "+v"(m_lo));
     asm volatile("" : "+v"(m_hi));
   }
@@ -557,6 +573,24 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           }
           cs = 1032.0f * lo + 1152.0f * hi;
           *px = y;
+        } else if constexpr (kSplitB) {
+          const u32x4_t x = y;
+          y[0] = __builtin_amdgcn_perm(x[2], x[0], 0x05040100u);
+          y[1] = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);
+          y[2] = __builtin_amdgcn_perm(x[3], x[1], 0x05040100u);
+          y[3] = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);
+          float lo = 0.0f, hi = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const float v = __uint_as_float(y[c] << 16) + __uint_as_float(y[c] & 0xFFFF0000u);
+            if (c & 1) hi += v;
+            else lo += v;
+          }
+          // even k: x (128 + q) = x (q - 8) + 136 x; odd k: (x / 8)(128 + 8 q) = x (q - 8) + 24 x
+          cs = 136.0f * lo + 24.0f * hi;
+          y[1] = bf16x2_eighth(y[1]);
+          y[3] = bf16x2_eighth(y[3]);
+          *px = y;
         } else {
           float sum = 0.0f;
 #pragma unroll
@@ -645,6 +679,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           for (int u = 0; u < WT; ++u) {
             u32x4_t bw;
             if constexpr (kSplit) bw = dq4_f16_split(wq[u][0][st], m_lo, m_hi);
+            else if constexpr (kSplitB) bw = dq4_bf16_split(wq[u][0][st], m_lo, m_hi);
             else bw = weight_biased<AT, WF>(wq[u], st);
             acc[u] += mfma16x16x32<AT>(av, bw, zero) * s4[u][st];
           }
@@ -663,6 +698,8 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
           u32x4_t bw;
           if constexpr (kSplit) {
             bw = dq4_f16_split(d.w[u][0][st], m_lo, m_hi);
+          } else if constexpr (kSplitB) {
+            bw = dq4_bf16_split(d.w[u][0][st], m_lo, m_hi);
           } else if constexpr (kBiased) {
             bw = weight_biased<AT, WF>(d.w[u], st);
           } else {
