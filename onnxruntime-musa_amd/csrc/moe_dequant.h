@@ -255,6 +255,25 @@ __device__ __forceinline__ u32x4_t weight_biased(const u32x4_t* v, int s) {
   }
 }
 
+// MXFP4 (OCP MX v1.0 FP4 E2M1, even k in the low nibble) dword (k0..k7) ->
+// 16-bit pairs (k0 k1) .. (k6 k7) of e2m1(nibble) * sc, with the gfx950
+// FP4 conversion (one instruction per byte).  Every E2M1 value times a
+// power of two is exact in fp16 / bf16 inside the type's range.
+template <typename AT>
+__device__ __forceinline__ u32x4_t fp4_scaled(uint32_t v, float sc) {
+  if constexpr (AT::kId == 10) {
+    return u32x4_t{h2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 0)),
+                   h2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 1)),
+                   h2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 2)),
+                   h2_bits(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 3))};
+  } else {
+    return u32x4_t{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 0)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 1)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 2)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, sc, 3))};
+  }
+}
+
 // Weight row (within one expert) that tile t of feature f reads.
 __device__ __forceinline__ int64_t tile_row(int64_t f, bool lin, bool fc1_gated, int gate_mode, int64_t nfeat) {
   if (fc1_gated && gate_mode == kGateInterleaved) return 2 * f + (lin ? 1 : 0);

@@ -23,6 +23,20 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 struct F32 { using storage = float; static constexpr int kId = 1; };
 struct F16 { using storage = _Float16; static constexpr int kId = 10; };
 struct BF16 { using storage = uint16_t; static constexpr int kId = 16; };
+// OCP Microscaling (MX v1.0) E8M0 block scale: 2^(e - 127), e = 255 is NaN.
+struct E8M0 { using storage = uint8_t; static constexpr int kId = 2; };
+
+__device__ __forceinline__ float e8m0_to_f32(uint32_t e) {
+  return e == 0 ? __uint_as_float(0x00400000u) : (e == 255 ? __uint_as_float(0x7FC00000u) : __uint_as_float(e << 23));
+}
+
+// OCP MX FP4 E2M1 element (sign, 2 exponent bits with bias 1, 1 mantissa
+// bit): 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives.
+__device__ __forceinline__ float e2m1_to_f32(uint32_t n) {
+  const uint32_t e = (n >> 1) & 3u, m = n & 1u;
+  const float mag = e == 0 ? 0.5f * static_cast<float>(m) : __builtin_ldexpf(1.0f + 0.5f * static_cast<float>(m), static_cast<int>(e) - 1);
+  return (n & 8u) ? -mag : mag;
+}
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
@@ -41,6 +55,8 @@ template <>
 __device__ __forceinline__ float to_f32<F16>(_Float16 v) { return static_cast<float>(v); }
 template <>
 __device__ __forceinline__ float to_f32<BF16>(uint16_t v) { return bf16_to_f32(v); }
+template <>
+__device__ __forceinline__ float to_f32<E8M0>(uint8_t v) { return e8m0_to_f32(v); }
 
 template <typename Tag>
 __device__ __forceinline__ typename Tag::storage from_f32(float v);

@@ -65,7 +65,9 @@ __device__ __forceinline__ u32x4_t bload16_aux(__amdgpu_buffer_rsrc_t r, uint32_
 // kScaleStep (stream kernel, block 32 / 64): each MFMA step takes 32
 // consecutive k, which lie in one scale block, so the operands stay exact
 // (biased) integers and the block scale multiplies the step's fp32 result.
-enum ScaleMode : int { kScaleNone = 0, kScaleChan = 1, kScaleBlock = 2, kScaleFold = 3, kScaleStep = 4 };
+// kScaleMx (stream kernel, MXFP4): the same step-major k; each step's E2M1
+// operands are converted with the E8M0 scale of its block folded in.
+enum ScaleMode : int { kScaleNone = 0, kScaleChan = 1, kScaleBlock = 2, kScaleFold = 3, kScaleStep = 4, kScaleMx = 5 };
 
 struct Stage {
   const void* in;  // fc1: x [T, K]; fc2: act [T*k, K]

@@ -112,6 +112,11 @@ bool decode_supported(const ExpertArgs& a) {
   const int64_t lim = int64_t{1} << 31;
   if (n1 * a.H / 2 * wb >= lim || a.H * a.I / 2 * wb >= lim) return false;
   if (a.T * a.k * std::max(a.H, a.I) * 2 >= lim) return false;
+  // MXFP4: the stream kernels only (both stages)
+  if (a.mx) {
+    const DecodePlan pl = plan_decode(a.T, a.H, a.I, a.E, a.k, a.wfmt, a.gate_mode);
+    if (!pl.stream1 || !pl.stream2) return false;
+  }
   return true;
 }
 

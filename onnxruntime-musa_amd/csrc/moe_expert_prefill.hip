@@ -31,6 +31,7 @@
 //  * fc2 may split K across workgroups; the partial sums land in separate
 //    fp32 planes of y2 that finalize adds in a fixed order.
 #include <algorithm>
+#include <type_traits>
 
 #include "moe_dequant.h"
 #include "moe_launch.h"
@@ -245,6 +246,18 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
       if (s_aligned) {
         swin = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs_sg, static_cast<int>(og), 0, 0)) |
                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs_sl, static_cast<int>(ol), 0, 0));
+      } else if constexpr (SB == 1) {
+        // 1-byte (E8M0) scales: rows start at any byte
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            w |= static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(rs_sg, static_cast<int>(og + 4 * q + b), 0, 0) |
+                                       __builtin_amdgcn_raw_buffer_load_b8(rs_sl, static_cast<int>(ol + 4 * q + b), 0, 0))
+                 << (8 * b);
+          swin[q] = w;
+        }
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -301,6 +314,11 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   // Weight operand of block j, step s: 8 k as 16-bit values; sc: the block
   // scale of the step.
   auto bop = [&](const Ring& d, int j, int s, float sc) -> u32x4_t {
+    if constexpr (std::is_same_v<ST, E8M0>) {
+      // MXFP4: E2M1 pairs times the power-of-two block scale in one
+      // conversion each (exact within the 16-bit type's range)
+      return fp4_scaled<AT>(d.w[j][s >> 2][s & 3], sc);
+    }
     u32x4_t q;
     if constexpr (WF == kInt4) q = dq4_exact<AT>(d.w[j][s >> 2][s & 3]);
     else if constexpr (WF == kInt8) q = dq8_exact<AT>(d.w[j][s >> 1][(s & 1) * 2], d.w[j][s >> 1][(s & 1) * 2 + 1]);
@@ -553,6 +571,9 @@ hipError_t launch_scaled(const PStage& st, const ExpertArgs& a, bool gated, hipS
       if (nsc == 2) return launch_kernel<AT, WF, kPsBlock, ST, 2, FC1>(st, gated, stream);
       return launch_kernel<AT, WF, kPsBlock, ST, 1, FC1>(st, gated, stream);
     };
+    if constexpr (WF == kInt4) {
+      if (a.mx) return launch_kernel<AT, WF, kPsBlock, E8M0, 2, FC1>(st, gated, stream);  // block 32
+    }
     if (a.scale_type == MOE_ELEM_FLOAT) return by_type(F32{});
     if (a.scale_type == MOE_ELEM_BFLOAT16) return by_type(BF16{});
     return by_type(F16{});

@@ -18,11 +18,17 @@ struct WeightView {
   const void* s;
   int32_t wfmt, act_type, scale_type;
   int64_t N, K, block_size;
+  int32_t mx;  // MXFP4: E2M1 nibbles, E8M0 scale bytes per block of 32
 
   __device__ __forceinline__ float get(int64_t e, int64_t n, int64_t kk) const {
     if (wfmt == kDense) return load_any(w, act_type, (e * N + n) * K + kk);
     const uint8_t* q = static_cast<const uint8_t*>(w);
     const int64_t nblk = block_size > 0 ? K / block_size : 1;
+    if (mx) {
+      const uint8_t b = q[(e * N + n) * (K / 2) + (kk >> 1)];
+      const uint8_t sc = static_cast<const uint8_t*>(s)[(e * N + n) * nblk + kk / block_size];
+      return e2m1_to_f32((kk & 1) ? (b >> 4) : (b & 0x0F)) * e8m0_to_f32(sc);
+    }
     const float sc =
         load_any(s, scale_type, (e * N + n) * nblk + (block_size > 0 ? kk / block_size : 0));
     int v;
@@ -55,8 +61,8 @@ __global__ void __launch_bounds__(256) fc1_simt_kernel(ExpertArgs a) {
   if (a.gate_mode == kGateInterleaved) { ng = 2 * i; nl = 2 * i + 1; }
   else if (a.gate_mode == kGateChunked) { ng = i; nl = a.I + i; }
   else if (a.gate_mode == kGateFc3) { ng = i; nl = i; }
-  const WeightView w1{a.w1, a.s1, a.wfmt, a.act_type, a.scale_type, N1, a.H, a.block_size};
-  const WeightView w3{a.w3, a.s3, a.wfmt, a.act_type, a.scale_type, a.I, a.H, a.block_size};
+  const WeightView w1{a.w1, a.s1, a.wfmt, a.act_type, a.scale_type, N1, a.H, a.block_size, a.mx};
+  const WeightView w3{a.w3, a.s3, a.wfmt, a.act_type, a.scale_type, a.I, a.H, a.block_size, a.mx};
   float sg = 0.0f, sl = 0.0f;
   for (int64_t kk = lane; kk < a.H; kk += kWave) {
     const float xv = load_act(a.x, a.act_type, tok * a.H + kk);
@@ -88,7 +94,7 @@ __global__ void __launch_bounds__(256) fc2_simt_kernel(ExpertArgs a) {
   const int64_t r = blockIdx.x;
   if (h >= a.H) return;
   const int64_t e = a.topk_ids[a.perm[r]];
-  const WeightView w2{a.w2, a.s2, a.wfmt, a.act_type, a.scale_type, a.H, a.I, a.block_size};
+  const WeightView w2{a.w2, a.s2, a.wfmt, a.act_type, a.scale_type, a.H, a.I, a.block_size, a.mx};
   float s = 0.0f;
   for (int64_t kk = lane; kk < a.I; kk += kWave)
     s += load_act(a.act, a.act_type, r * a.I + kk) * w2.get(e, h, kk);

@@ -108,7 +108,9 @@ struct ScaleRaw {
   using type = std::conditional_t<(kBytes > 8), u32x4_t, std::conditional_t<(kBytes > 4), u32x2_t, uint32_t>>;
   template <int AUX>
   __device__ static __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    if constexpr (kBytes == 2) {
+    if constexpr (kBytes == 1) {
+      return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b8(r, static_cast<int>(off), 0, AUX));
+    } else if constexpr (kBytes == 2) {
       return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, AUX));
     } else if constexpr (kBytes == 4) {
       return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, AUX);
@@ -119,7 +121,10 @@ struct ScaleRaw {
     }
   }
   __device__ static __forceinline__ float elem(type v, int i) {
-    if constexpr (std::is_same_v<ST, F32>) {
+    if constexpr (std::is_same_v<ST, E8M0>) {
+      (void)i;
+      return e8m0_to_f32(v & 0xFFu);
+    } else if constexpr (std::is_same_v<ST, F32>) {
       if constexpr (kBytes == 4) return __uint_as_float(v);
       else return __uint_as_float(v[i]);
     } else {
@@ -245,11 +250,13 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   constexpr int kAux = STREAM_NT ? kStreamAux : 0;
   constexpr int NW = G::NW, NT = NW * 64, WT = G::WT, FT = G::FT, PD = G::PD, LB = G::kLaneBytes;
   constexpr bool kStep = SM == kScaleStep;
+  constexpr bool kMx = SM == kScaleMx;  // MXFP4: step-major, E2M1 operands, E8M0 step scales
+  static_assert(!kMx || (WF == kInt4 && std::is_same_v<ST, E8M0> && NSC == 1), "MXFP4: 4-bit E2M1, E8M0 scales");
   constexpr bool kBiased = Biased<AT, WF>::kOk && (SM == kScaleBlock || SM == kScaleChan || kStep);
   static_assert(!kStep || (Biased<AT, WF>::kOk && NSC == 1), "step scales: biased operands, one scale per lane");
   constexpr bool kSplit = kBiased && WF == kInt4 && AT::kId == 10;
   constexpr bool kSplitB = kBiased && WF == kInt4 && AT::kId == 16;
-  constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold || kStep;
+  constexpr bool kRingScales = SM == kScaleBlock || SM == kScaleFold || kStep || kMx;
   constexpr bool kGroupScales = SM == kScaleBlock && NSC == 4;
   // 2-byte block scales of block 128 are loaded per tile: one load per
   // lane (row col, lane group g) brings the 16 bytes that hold the scales
@@ -387,7 +394,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // the weights'); nblk_r: their elements per row, with K padded to whole
   // chunks.  One load instruction then reads 16 * nbc * 2 (or 4) bytes in
   // one run instead of one cache line per row.
-  const bool stiled = kStep && tiled && p.stiled != 0;
+  const bool stiled = (kStep || kMx) && tiled && p.stiled != 0;
   const int nbc = kChunk >> bshift;
   const uint32_t nblk_r = stiled ? static_cast<uint32_t>(nchunks * nbc) : nblk;
   // Tile-major weights (pre-packed; weight tiles start at a multiple of 16
@@ -491,7 +498,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
                                                       v * vdelta, kAux));
         if constexpr (kRingScales && !kTileScales) {
           // folded and step scales: the block of lane group g's 32 k
-          constexpr bool kPerGroup = SM == kScaleFold || kStep;
+          constexpr bool kPerGroup = SM == kScaleFold || kStep || kMx;
           const uint32_t kk = static_cast<uint32_t>(cg) * kChunk + (kPerGroup ? 32 * g : 0);
           // a block scale multiplies the whole chunk's sum (every lane group
           // of the MFMA output), so only a chunk past K reads none
@@ -631,6 +638,32 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     u32x2_t bsc[WT];
     auto compute = [&](int cl, int slot) {
       const CK& d = ring[slot];
+      if constexpr (kMx) {
+        // MXFP4: step st takes k [32 st, 32 st + 32), one E8M0 block, whose
+        // power-of-two scale the FP4 conversion applies (exact for bf16, and
+        // for fp16 while the scaled weight is an fp16 normal); the MFMA
+        // accumulates straight into acc
+        const uint8_t* xr = xs + col * pitch + cl * 256 + g * 16;
+        u32x4_t wq[WT];
+        float s4[WT][4];
+#pragma unroll
+        for (int u = 0; u < WT; ++u) {
+          uint32_t v[4] = {d.w[u][0][0], d.w[u][0][1], d.w[u][0][2], d.w[u][0][3]};
+          transpose_rows4(v);
+          wq[u] = u32x4_t{v[0], v[1], v[2], v[3]};
+          uint32_t g4[4];
+          gather_rows4(__float_as_uint(SR::elem(d.sc[u], 0)), g4);
+#pragma unroll
+          for (int st = 0; st < 4; ++st) s4[u][st] = __uint_as_float(g4[st]);
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xr + 64 * st);
+#pragma unroll
+          for (int u = 0; u < WT; ++u) acc[u] = mfma16x16x32<AT>(av, fp4_scaled<AT>(wq[u][st], s4[u][st]), acc[u]);
+        }
+        return;
+      }
       if constexpr (kStep) {
         // Step st: k [32 st, 32 st + 32) of the chunk, one scale block.  The
         // result is sum_st s_st * (mfma_st - c_st): the products s_st * mfma_st
@@ -966,6 +999,12 @@ hipError_t launch_stream_fmt(const StreamStage& ss, const ExpertArgs& a, bool fc
       // block 128 and K a multiple of 512: 4 chunks' scales are one aligned load
       if (a.block_size == 128 && ss.s.K % 512 == 0) return bf ? by_st(BF16{}, BLK{}, FOUR{}) : by_st(F16{}, BLK{}, FOUR{});
       return bf ? by_st(BF16{}, BLK{}, ONE{}) : by_st(F16{}, BLK{}, ONE{});
+    }
+    if constexpr (WF == kInt4) {
+      if (a.mx) {  // MXFP4: E8M0 scales of block 32
+        return bf ? launch_stream_kinds<BF16, WF, kScaleMx, E8M0, 1>(ss, fc1, gated, stream)
+                  : launch_stream_kinds<F16, WF, kScaleMx, E8M0, 1>(ss, fc1, gated, stream);
+      }
     }
     // blocks of 32 / 64 with a biased operand form: step scales
     using STEP = std::integral_constant<int, kScaleStep>;

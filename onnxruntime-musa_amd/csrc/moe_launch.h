@@ -84,6 +84,10 @@ struct ExpertArgs {
   int32_t deint1;
   // 1: the stage's block scales (block 32 / 64) are tile-major too
   int32_t stiled1, stiled2;
+  // 1: MXFP4 experts (OCP MX v1.0): wfmt kInt4's packing (two elements per
+  // byte, even k low) of FP4 E2M1 values, scale_type uint8 E8M0 block
+  // scales of block_size 32
+  int32_t mx;
   // intermediates
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
@@ -127,7 +131,7 @@ hipError_t launch_softmax(const void* in, void* out, int32_t elem_type, int64_t 
 // split into halves when deint (expert_rows a multiple of 32).
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
                           int64_t expert_rows, bool deint, hipStream_t stream);
-// Reorders block scales [rows, nblk] of block 32 or 64 (elem_bytes 2 or 4)
+// Reorders block scales [rows, nblk] of block 32 or 64 (elem_bytes 1, 2 or 4)
 // into the tile-major layout of the step-scale decode kernels: per (16-row
 // tile, chunk of 128 k) the 16 rows' 128 / block scales, blocks past K zero,
 // rows de-interleaved like their weights when deint (moe_prepack.hip).

@@ -63,6 +63,7 @@ std::string dims_str(const moe_tensor& t) {
 struct Problem {
   int64_t T = 0, H = 0, I = 0, E = 0, k = 0, N1 = 0;
   int32_t act_type = 0, scale_type = MOE_ELEM_FLOAT16, wfmt = moe::kDense, gate_mode = moe::kGateNone;
+  int32_t mx = 0;  // MXFP4 experts: uint8 (E8M0) scales with 4-bit weights, block 32
   int64_t block_size = 0;
   const moe_tensor* in[11] = {};
 };
@@ -200,9 +201,16 @@ moe_status validate(const moe_kernel* kr, const moe_tensor* inputs, int32_t n, P
         (w3 && w3->elem_type != MOE_ELEM_UINT8))
       return fail(MOE_INVALID_ARGUMENT, "QMoE expert weights must be uint8");
     p.scale_type = s1->elem_type;
-    if (!is_float_type(p.scale_type) || s2->elem_type != p.scale_type ||
+    // uint8 scales: MXFP4 experts (OCP MX v1.0 FP4 E2M1 elements, E8M0
+    // scales per 32 k), a library extension beyond the 1.26 QMoE schema,
+    // whose scale type T2 is a float type
+    p.mx = p.scale_type == MOE_ELEM_UINT8 ? 1 : 0;
+    if ((!is_float_type(p.scale_type) && !p.mx) || s2->elem_type != p.scale_type ||
         (s3 && s3->elem_type != p.scale_type))
-      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must share one float type");
+      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must share one float type (or uint8 E8M0 for MXFP4)");
+    if (p.mx && (at.expert_weight_bits != 4 || at.block_size != 32))
+      return fail(MOE_INVALID_ARGUMENT, "MXFP4 experts (uint8 E8M0 scales) need expert_weight_bits 4 and "
+                                        "block_size 32");
     p.block_size = at.block_size;
   } else {
     if (w1->elem_type != p.act_type || w2->elem_type != p.act_type ||
@@ -328,11 +336,13 @@ bool env_set(const char* name) {
 size_t prepack_scale_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* s, int32_t act_type) {
   const moe_attributes& at = kr->attrs;
   const int64_t bs = at.block_size;
+  const bool mx = s->elem_type == MOE_ELEM_UINT8;  // MXFP4 E8M0 scales (block 32)
   if (bs != 32 && bs != 64) return 0;
+  if (mx && (bs != 32 || at.expert_weight_bits != 4)) return 0;
   if (act_type != MOE_ELEM_FLOAT16 && act_type != MOE_ELEM_BFLOAT16) return 0;
-  if (at.expert_weight_bits == 8 && act_type != MOE_ELEM_FLOAT16) return 0;
+  if (!mx && at.expert_weight_bits == 8 && act_type != MOE_ELEM_FLOAT16) return 0;
   const int64_t E = s->dims[0], N = s->dims[1], nblk = s->dims[2];
-  const int64_t es = s->elem_type == MOE_ELEM_FLOAT ? 4 : 2;
+  const int64_t es = s->elem_type == MOE_ELEM_FLOAT ? 4 : (mx ? 1 : 2);
   if (N <= 0 || N % 16 || nblk <= 0) return 0;
   const int64_t nchunks = (nblk * bs + 127) / 128;
   const int64_t cbytes = at.expert_weight_bits == 4 ? 64 : 128;
@@ -357,8 +367,9 @@ moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w,
   if (!kr->quantized) return MOE_OK;
   if (scales) {
     // per output channel [E, N] (kept as given) or per block [E, N, K / block]
-    if ((w->rank != 2 && w->rank != 3) || !is_float_type(w->elem_type) || w->dims[0] <= 0)
-      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must be 2D or 3D float, got " + dims_str(*w));
+    if ((w->rank != 2 && w->rank != 3) || (!is_float_type(w->elem_type) && w->elem_type != MOE_ELEM_UINT8) ||
+        w->dims[0] <= 0)
+      return fail(MOE_INVALID_ARGUMENT, "QMoE scales must be 2D or 3D float (or uint8 E8M0), got " + dims_str(*w));
     if (w->rank == 3) *bytes = prepack_scale_bytes(kr, idx, w, act_type);
     return MOE_OK;
   }
@@ -420,6 +431,7 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   a.deint1 = a.tiled1 && kr->packed[2].deint ? 1 : 0;
   a.stiled1 = q && kr->packed[3].data ? 1 : 0;
   a.stiled2 = q && kr->packed[6].data ? 1 : 0;
+  a.mx = p.mx;
   a.act = ws + l.act;
   a.y2 = reinterpret_cast<float*>(ws + l.y2);
   a.y2_planes = 1;
@@ -555,7 +567,9 @@ moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe
     const bool deint = prepack_deint(kernel, input_index);
     const bool scales = input_index == 3 || input_index == 6 || input_index == 9;
     const hipError_t e =
-        scales ? moe::launch_prepack_scales(weights->data, dst, weights->elem_type == MOE_ELEM_FLOAT ? 4 : 2,
+        scales ? moe::launch_prepack_scales(weights->data, dst,
+                                            weights->elem_type == MOE_ELEM_FLOAT ? 4
+                                                : (weights->elem_type == MOE_ELEM_UINT8 ? 1 : 2),
                                             weights->dims[0] * weights->dims[1], weights->dims[2],
                                             static_cast<int>(kernel->attrs.block_size), weights->dims[1], deint,
                                             static_cast<hipStream_t>(stream))

@@ -81,7 +81,8 @@ __global__ void __launch_bounds__(256) prepack_scales_kernel(const E* __restrict
 
 hipError_t launch_prepack_scales(const void* src, void* dst, int elem_bytes, int64_t rows, int64_t nblk, int block,
                                  int64_t expert_rows, bool deint, hipStream_t stream) {
-  if (rows % 16 || (block != 32 && block != 64) || (elem_bytes != 2 && elem_bytes != 4) || expert_rows <= 0 ||
+  if (rows % 16 || (block != 32 && block != 64) || (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4) ||
+      expert_rows <= 0 ||
       rows % expert_rows || (deint && expert_rows % 32))
     return hipErrorInvalidValue;
   const int nb = 128 / block;
@@ -90,7 +91,11 @@ hipError_t launch_prepack_scales(const void* src, void* dst, int elem_bytes, int
   if (nelems == 0) return hipSuccess;
   const int64_t want = (nelems + 255) / 256;
   const unsigned blocks = static_cast<unsigned>(want < 65536 ? want : 65536);
-  if (elem_bytes == 2)
+  if (elem_bytes == 1)
+    hipLaunchKernelGGL(prepack_scales_kernel<uint8_t>, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), nelems, nchunks, nb, nblk,
+                       expert_rows, deint ? 1 : 0);
+  else if (elem_bytes == 2)
     hipLaunchKernelGGL(prepack_scales_kernel<uint16_t>, dim3(blocks), dim3(256), 0, stream,
                        static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), nelems, nchunks, nb, nblk,
                        expert_rows, deint ? 1 : 0);

@@ -13,6 +13,12 @@ s = max|w_row| / 127, q = clamp(round(w / s), -128, 127) + 128; int4 per block
 of `block_size` along K, s = max|w_block| / 7, q = clamp(round(w / s), -8, 7) + 8,
 two values per byte with the even-k value in the low nibble.
 
+MXFP4 (OCP Microscaling Formats v1.0; the library extension for gpt-oss
+style experts): per block of 32 along K a shared E8M0 exponent
+e = floor(log2 max|w|) - 2 (uint8 scale byte e + 127), elements w / 2^e
+rounded to the nearest FP4 E2M1 value (ties to the even code, saturating at
++-6), two per byte with the even-k element in the low nibble.
+
 Zipf routing (the Qwen3-MoE-shaped config): p_e ~ r_e^-s with r a seeded
 permutation of 1..E, logits = log p_e + Gumbel(0, 1); by the Gumbel-top-k trick
 each token's top-k is a draw without replacement proportional to p.
@@ -41,7 +47,8 @@ class MoEConfig:
     dtype: str = "f16"           # activation / bias type T
     bits: int = 0                # 0 = MoE (float weights); 4 / 8 = QMoE
     block_size: int = 0          # 0 = per output channel
-    scale_dtype: str = "f16"     # T2
+    scale_dtype: str = "f16"     # T2 ("e8m0": uint8 MXFP4 scales)
+    weight_format: str = "int"   # "int" (QMoE zero-point integers) | "mxfp4" (bits 4, block 32, e8m0)
     activation: str = "swiglu"
     swiglu_fusion: int = 0       # 0 with use_fc3, 1 interleaved, 2 chunked
     use_fc3: bool = True
@@ -71,7 +78,7 @@ class MoEConfig:
         """HBM bytes of one expert's weights, scales and biases."""
         H, I, n1 = self.hidden, self.inter, self.n1
         rows_k = [(n1, H), (H, I)] + ([(I, H)] if self.use_fc3 else [])
-        esz = {"f32": 4, "f16": 2, "bf16": 2}
+        esz = {"f32": 4, "f16": 2, "bf16": 2, "e8m0": 1}
         total = 0
         for n, kk in rows_k:
             if self.bits == 0:
@@ -118,6 +125,12 @@ CONFIGS: Dict[str, MoEConfig] = {
     # MoE fp16, Qwen3-MoE shape, Zipf-skewed routing
     "c5_moe_f16_qwen3": MoEConfig("c5_moe_f16_qwen3", hidden=2048, inter=768, experts=128, k=8, dtype="f16",
                                   router="zipf", tokens=(8192,)),
+    # extension (not a BASELINE config): configs[3]'s gpt-oss shape with MXFP4
+    # experts (E2M1 elements, E8M0 block-32 scales), the format gpt-oss ships
+    "x1_mxfp4_gptoss": MoEConfig("x1_mxfp4_gptoss", hidden=2880, inter=2880, experts=32, k=4,
+                                 dtype="bf16", bits=4, block_size=32, scale_dtype="e8m0", weight_format="mxfp4",
+                                 swiglu_fusion=1, use_fc3=False, swiglu_limit=7.0, alpha=1.702, beta=1.0,
+                                 bias=True, tokens=(1, 16, 64, 8192)),
 }
 
 
@@ -155,6 +168,27 @@ def quantize_int8_block(w: torch.Tensor, block: int, scale_dtype: torch.dtype):
     safe = torch.where(s > 0, s, torch.ones_like(s))
     q = (torch.clamp(torch.round(wb / safe.unsqueeze(-1)), -128, 127) + 128).to(torch.uint8).reshape(*lead, N, K)
     return q.contiguous(), s.to(scale_dtype)
+
+
+_E2M1_GRID = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def quantize_mxfp4(w: torch.Tensor):
+    """w [..., N, K] float -> (packed uint8 [..., N, K/2] E2M1 nibbles,
+    uint8 [..., N, K/32] E8M0 scales), the MX v1.0 quantizer."""
+    *lead, N, K = w.shape
+    wb = w.reshape(*lead, N, K // 32, 32).to(torch.float64)
+    amax = wb.abs().amax(dim=-1)
+    e = torch.where(amax > 0, torch.floor(torch.log2(amax.clamp_min(2.0 ** -200))) - 2,
+                    torch.full_like(amax, -127.0)).clamp(-127, 127)
+    a = (wb.abs() / torch.exp2(e).unsqueeze(-1)).clamp(max=6.0)
+    grid = torch.tensor(_E2M1_GRID, dtype=torch.float64, device=w.device)
+    # nearest grid value; a tie goes to the even code (odd codes lose by 1e-9)
+    odd = (torch.arange(8, device=w.device) % 2).to(torch.float64) * 1e-9
+    code = ((a.unsqueeze(-1) - grid).abs() + odd).argmin(dim=-1)
+    nib = (code | ((wb < 0).to(torch.int64) << 3)).to(torch.uint8).reshape(*lead, N, K)
+    packed = nib[..., 0::2] | (nib[..., 1::2] << 4)
+    return packed.contiguous(), (e + 127).to(torch.uint8).contiguous()
 
 
 def quantize(w: torch.Tensor, bits: int, block: int, scale_dtype: torch.dtype):
@@ -225,7 +259,10 @@ def make_problem(cfg: MoEConfig, tokens: int, seed: int = 0, device="cuda", gen:
     d = _Draw(gen, seed, device)
     T, H, I, E, n1 = tokens, cfg.hidden, cfg.inter, cfg.experts, cfg.n1
     dt = _TORCH_DT[cfg.dtype]
-    sdt = _TORCH_DT[cfg.scale_dtype]
+    mx = cfg.weight_format == "mxfp4"
+    if mx and (cfg.bits != 4 or cfg.block_size != 32):
+        raise ValueError("MXFP4 experts need bits 4 and block_size 32")
+    sdt = None if mx else _TORCH_DT[cfg.scale_dtype]
     p = Problem(cfg, tokens, seed)
     p.inputs["input"] = d.normal((T, H)).to(dt).contiguous()
     if cfg.router == "zipf":
@@ -243,7 +280,7 @@ def make_problem(cfg: MoEConfig, tokens: int, seed: int = 0, device="cuda", gen:
         mats = [d.normal((n, kk), 1.0 / math.sqrt(kk)) for _ in range(E)]
         if cfg.bits == 0:
             return torch.stack([m.to(dt) for m in mats]).contiguous(), None
-        qs = [quantize(m, cfg.bits, cfg.block_size, sdt) for m in mats]
+        qs = [quantize_mxfp4(m) if mx else quantize(m, cfg.bits, cfg.block_size, sdt) for m in mats]
         return torch.stack([q for q, _ in qs]).contiguous(), torch.stack([s for _, s in qs]).contiguous()
 
     def bias(n, fan_in):
@@ -274,4 +311,4 @@ def to_host(t: Optional[torch.Tensor]) -> Optional[np.ndarray]:
     return t.numpy()
 
 
-__all__ = ["MoEConfig", "CONFIGS", "Problem", "make_problem", "quantize", "to_host"]
+__all__ = ["MoEConfig", "CONFIGS", "Problem", "make_problem", "quantize", "quantize_mxfp4", "to_host"]

@@ -270,7 +270,9 @@ def forward_problem(cfg, host: dict, token_mask=None, threads=0):
         act_dtype=cfg.dtype, activation=cfg.activation, normalize=cfg.normalize, swiglu_fusion=cfg.swiglu_fusion,
         swiglu_limit=cfg.swiglu_limit, alpha=cfg.alpha, beta=cfg.beta,
         router_sigmoid=getattr(cfg, "router_sigmoid", 0), bits=cfg.bits, block_size=cfg.block_size,
-        scale_dtype=cfg.scale_dtype, s1=host.get("fc1_scales"), b1=host.get("fc1_experts_bias"),
+        # (MXFP4 E8M0 scale bytes are read per weight_format; the type is unused)
+        scale_dtype=cfg.scale_dtype if cfg.scale_dtype in _DT else "f32",
+        s1=host.get("fc1_scales"), b1=host.get("fc1_experts_bias"),
         s2=host.get("fc2_scales"), b2=host.get("fc2_experts_bias"), w3=host.get("fc3_experts_weights"),
         s3=host.get("fc3_scales"), b3=host.get("fc3_experts_bias"), token_mask=token_mask, threads=threads,
         weight_format=1 if getattr(cfg, "weight_format", "int") == "mxfp4" else 0)

@@ -201,6 +201,8 @@ def mutate(ins, i, **kw):
     (lambda b: mutate(b, 2, et=C.ELEM_FLOAT16), C.MOE_INVALID_ARGUMENT),         # QMoE weights not uint8
     (lambda b: mutate(b, 2, dims=[8, 512, 256]), C.MOE_INVALID_ARGUMENT),        # fc1 K not packed
     (lambda b: mutate(b, 3, dims=[8, 512, 4]), C.MOE_INVALID_ARGUMENT),          # fc1 scale blocks wrong
+    (lambda b: mutate(mutate(mutate(b, 3, et=C.ELEM_UINT8), 6, et=C.ELEM_UINT8), 9, et=C.ELEM_UINT8),
+     C.MOE_INVALID_ARGUMENT),                                                    # E8M0 (MXFP4) with block 128
     (lambda b: mutate(b, 6, et=C.ELEM_FLOAT), C.MOE_INVALID_ARGUMENT),           # scale types differ
     (lambda b: mutate(b, 8, dims=[8, 256, 128]), C.MOE_INVALID_ARGUMENT),        # fc3 shape
     (lambda b: mutate(b, 9, data=None), C.MOE_INVALID_ARGUMENT),                 # fc3 without scales
@@ -313,6 +315,8 @@ def test_prepack_size_rules(lib, bits, idx, dims, packed_rb):
     (4, 16, C.ELEM_FLOAT16, 3, [8, 512, 16], C.ELEM_FLOAT16, 0),   # block 16: folded
     (4, 32, C.ELEM_FLOAT16, 3, [8, 520, 8], C.ELEM_FLOAT16, 0),    # N not a multiple of 16
     (4, 32, C.ELEM_FLOAT16, 6, [8, 512], C.ELEM_FLOAT16, 0),       # per-channel scales stay as given
+    (4, 32, C.ELEM_BFLOAT16, 3, [8, 5760, 90], C.ELEM_UINT8, 8 * 5760 * 23 * 4),  # MXFP4 E8M0 bytes
+    (4, 64, C.ELEM_BFLOAT16, 3, [8, 512, 4], C.ELEM_UINT8, 0),     # E8M0 needs block 32
 ])
 def test_prepack_size_scales(lib, bits, block, act, idx, dims, elem, packed):
     st, h = create(lib, "QMoE", k=2, activation_type=4, swiglu_fusion=1, block_size=block,
@@ -359,7 +363,7 @@ def test_prepack_size_fp32_activations_and_moe_stay_row_major(lib, qkernel):
 
 
 @pytest.mark.parametrize("idx,dims,et,act", [
-    (3, [8, 512, 128], C.ELEM_UINT8, C.ELEM_FLOAT16),   # scales that are not a float type
+    (3, [8, 512, 128], C.ELEM_INT32, C.ELEM_FLOAT16),   # scales neither float nor uint8 (E8M0)
     (6, [8, 512, 4, 1], C.ELEM_FLOAT16, C.ELEM_FLOAT16),  # scales neither 2D nor 3D
     (4, [8, 512], C.ELEM_FLOAT16, C.ELEM_FLOAT16),       # a bias input
     (0, [16, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16),

@@ -24,6 +24,12 @@ Each oracle function is checked against something that does not restate it:
                layout equivalences (fc1/fc3 unfused == fused chunked ==
                fused interleaved), QMoE == MoE on dequantised weights,
                single-expert == dense FFN, linearity in the fc2 scales
+  mxfp4        E2M1 / E8M0 known answers (all 16 codes, scale bytes 0, 126,
+               127, 128, 254, 255 = NaN), hand-packed bytes, a round trip
+               through the MX v1.0 quantizer written here in numpy (nearest
+               value within half a grid step, saturation past 6) with planted
+               nibble-order, sign and scale-bias mistakes, and the forward
+               against a float64 formulation decoding with numpy's own table
   fixtures     tests/golden/*.npz written by tests/golden/make_golden.py
 
 The "planted mistake" tests feed each check a plausible mistake (swapped tie
@@ -411,6 +417,22 @@ def test_mxfp4_quantizer_round_trip_and_planted_mistakes():
         assert _mxfp4_excess(oracle.dequant_mxfp4(qm, s, N, K), w, X) > 1.5, what
     assert _mxfp4_excess(oracle.dequant_mxfp4(q, (s + 1).astype(np.uint8), N, K), w, X) > 1.5, "scale bias 126"
     assert _mxfp4_excess(oracle.dequant_mxfp4(q, (s - 1).astype(np.uint8), N, K), w, X) > 1.5, "scale bias 128"
+
+
+def test_workload_mxfp4_quantizer_matches_spec():
+    """The benchmark's torch MXFP4 encoder produces the spec quantizer's bytes
+    (including ties, zero blocks and saturation)."""
+    import torch
+    from onnxruntime_musa_amd.workloads import quantize_mxfp4
+    rng = np.random.default_rng(21)
+    w = (rng.standard_normal((8, 128)) * 3).astype(np.float32)
+    w[0, :32] = 0.0                                                # zero block
+    w[1, :32] = np.float32([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0] * 4)  # ties at X = 1 (amax 6)
+    w[2, :32] = np.float32(2.0 ** np.arange(-16, 16))              # a wide block: small values round to 0
+    q, s = quantize_mxfp4(torch.from_numpy(w))
+    q_ref, s_ref, _ = _spec_quantize_mxfp4(w)
+    np.testing.assert_array_equal(q.numpy(), q_ref)
+    np.testing.assert_array_equal(s.numpy(), s_ref)
 
 
 def test_mxfp4_forward_matches_float64_formulation():
