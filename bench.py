@@ -49,12 +49,14 @@ CPU_PREFILL = ("c3_qmoe_int4_mixtral", 4096, 512)  # workload, tokens, tokens sa
 MALL_BYTES = 256 << 20  # MI355X Infinity Cache
 EXTRA = [("c2_qmoe_int8_mixtral", 1), ("c2_qmoe_int8_mixtral", 16), ("c2_qmoe_int8_mixtral", 4096),
          ("c3_qmoe_int4_mixtral", 1), ("c3_qmoe_int4_mixtral", 4096),
-         ("c4_qmoe_int4_gptoss", 1), ("c4_qmoe_int4_gptoss", 64), ("c4_qmoe_int4_gptoss", 8192),
-         ("c5_moe_f16_qwen3", 8192), ("c1_moe_f32", 64)]
+         ("c4_qmoe_int4_gptoss", 1), ("c4_qmoe_int4_gptoss", 16), ("c4_qmoe_int4_gptoss", 64),
+         ("c4_qmoe_int4_gptoss", 8192), ("c5_moe_f16_qwen3", 8192), ("c1_moe_f32", 64),
+         # extension: gpt-oss shape with MXFP4 experts (not a BASELINE config)
+         ("x1_mxfp4_gptoss", 16), ("x1_mxfp4_gptoss", 8192)]
 
 
 def esz(dt: str) -> int:
-    return 4 if dt == "f32" else 2
+    return {"f32": 4, "e8m0": 1}.get(dt, 2)
 
 
 def expert_bytes(cfg, part: str) -> int:

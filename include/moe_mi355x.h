@@ -21,6 +21,14 @@
  *        moe_kernel_release  <- OpKernelBase<Derived>::ReleaseImpl (kernel_base.h:86-89)
  *      Inputs are given in the op's schema order (MoE: 8 inputs, QMoE: 11).
  *
+ *      Extension beyond the 1.26 schema (whose QMoE scales T2 are float
+ *      types): QMoE with uint8 scales reads MXFP4 experts (OCP Microscaling
+ *      Formats v1.0, the format gpt-oss ships): expert weights are FP4 E2M1
+ *      values two per byte, even k in the low nibble (the int4 packing),
+ *      scales are E8M0 bytes (2^(e - 127), 0xFF = NaN) per block of 32 along
+ *      K; expert_weight_bits must be 4 and block_size 32, and the three
+ *      scale inputs must all be uint8.
+ *
  *   2. Stage launchers (moe_route_dispatch_launch): the device-launcher layer
  *      below a kernel, following the reference convention of POD params +
  *      device pointers + stream returning a runtime status
