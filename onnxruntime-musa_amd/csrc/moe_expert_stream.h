@@ -57,7 +57,7 @@ namespace decode {
 
 constexpr int kStreamRows = 16;       // token rows staged (the MFMA M dimension)
 constexpr int kStreamMaxChunks = 32;  // K chunks of one staged slice (16 x 32 x 256 B of LDS)
-constexpr int kStreamFetch = 4;       // chunks whose loads are issued back to back
+constexpr int kStreamFetch = 4;       // row-major weights: chunks whose loads are issued back to back
 static_assert(kStreamMaxChunks * kChunk == kStreamMaxK, "host and kernel agree on the slice size");
 
 // Chunks per block; a K slice is a whole number of blocks.
@@ -268,7 +268,15 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // before it, after that block has read the previous tile's scales.
   constexpr bool kTileScales = kGroupScales && sizeof(typename ST::storage) == 2;
   static_assert(!kTileScales || kStreamMaxChunks <= 32, "a slice's scales are 4 x 16 bytes per row");
-  static_assert(PD % kStreamFetch == 0, "a block is whole fetch groups");
+  // Chunks computed before their slots' next loads go out.  Row-major
+  // weights: kStreamFetch, so that one row's consecutive 64-byte pieces
+  // reach the memory controller together.  Tile-major weights (each load is
+  // one 1 KB run): every chunk's next load goes out as soon as the chunk is
+  // consumed, which keeps 3 of the 4 ring slots in flight while a
+  // VALU-heavy chunk computes; except with grouped block scales outside the
+  // tile-scale path, whose slot 0 holds the scales of the whole block.
+  constexpr int kFetch = STREAM_NT && !(kGroupScales && !kTileScales) ? 1 : kStreamFetch;
+  static_assert(PD % kFetch == 0, "a block is whole fetch groups");
   static_assert(!(SM == kScaleBlock && NSC == 4) || PD % 4 == 0, "grouped scales: 4 chunks of one block");
   using SR = ScaleRaw<ST, NSC>;
   using CK = SChunk<WF, GATED, SR, kRingScales>;
@@ -890,13 +898,12 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
 #pragma unroll
         for (int u = 0; u < WT; ++u) woff[u] = soff[u] = kOob;
       }
-      // chunks in groups of kStreamFetch: compute the group, then issue the
-      // loads of the same slots back to back (one row's consecutive 64-byte
-      // pieces reach the memory controller together)
+      // chunks in groups of kFetch: compute the group, then issue the loads
+      // of the same slots back to back
 #pragma unroll
-      for (int h = 0; h < PD; h += kStreamFetch) {
+      for (int h = 0; h < PD; h += kFetch) {
 #pragma unroll
-        for (int d = h; d < h + kStreamFetch; ++d) {
+        for (int d = h; d < h + kFetch; ++d) {
           compute(cb * PD + d, d);
           // keep each chunk's LDS reads and dequantisation next to its MFMAs
           __builtin_amdgcn_sched_barrier(0);
@@ -904,9 +911,9 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         // the next tile's scales, once this block (the last of its tile) has
         // read the current ones, ahead of the weights so that the next
         // block's wait for them leaves the weights in flight
-        if (kTileScales && h + kStreamFetch == PD && cb == bpt - 1 && bj + 1 < b1) fetch_tsc(tl + 1);
+        if (kTileScales && h + kFetch == PD && cb == bpt - 1 && bj + 1 < b1) fetch_tsc(tl + 1);
 #pragma unroll
-        for (int d = h; d < h + kStreamFetch; ++d) fetch(ncb * PD + d, woff, soff, ring[d]);
+        for (int d = h; d < h + kFetch; ++d) fetch(ncb * PD + d, woff, soff, ring[d]);
         __builtin_amdgcn_sched_barrier(0);
       }
       if (cb == bpt - 1 || bj == b1 - 1) {
