@@ -233,11 +233,13 @@ MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
  * weights, "ep.musa.enable_prepack_weight_sharing",
  * musa/ep/src/ep_factory.cc:472-478, musa/ep/src/ep.h:35).
  *
- * QMoE expert weights (input_index 2 fc1, 5 fc2, 8 fc3; `weights` is the
+ * Expert weights (QMoE input_index 2 fc1, 5 fc2, 8 fc3; MoE 2 fc1, 4 fc2, 6
+ * fc3, fp16 / bf16 weights of the activations' type; `weights` is the
  * constant initializer on the device) are reordered once into a tile-major
  * layout: each 16 rows x 128 k of an expert's [N, K/pack] matrix become one
- * contiguous block (1 KB int4, 2 KB int8), so that every load instruction
- * of the decode kernels reads one 1 KB run; K is padded with zeros to whole
+ * contiguous block (1 KB int4, 2 KB int8, 4 KB 16-bit), so that every
+ * weight load instruction of the decode and prefill kernels reads 1 KB
+ * runs rather than one cache line per row; K is padded with zeros to whole
  * chunks of 128, and the fused fc1 of interleaved SwiGLU is stored with its
  * gate rows first and its linear rows after.  Block scales of block size 32
  * or 64 (input_index 3 fc1, 6 fc2, 9 fc3; int4, or int8 with fp16
@@ -246,9 +248,10 @@ MOE_API moe_status moe_kernel_set_expert_path(moe_kernel *kernel, int32_t path);
  * input element type T (known from the node at kernel creation).
  *
  * moe_kernel_prepack_size: bytes of the packed copy, or 0 when the kernel
- *   reads that input in the op's layout (MoE, fp32 activations, N not a
- *   multiple of 16 (32 for a fused fc1), rows not whole 16-byte pieces,
- *   fc1/fc3 K above 4096, scales of other block sizes).
+ *   reads that input in the op's layout (fp32 activations, MoE weights not
+ *   of the activations' type, N not a multiple of 16 (32 for a fused fc1),
+ *   rows not whole 16-byte pieces, fc1/fc3 K above 4096, scales of other
+ *   block sizes).
  * moe_kernel_prepack: writes the packed copy into dst (device, at least that
  *   many bytes, 16-byte aligned) on stream, records dst and sets *is_packed.
  *   Every later compute (and workspace query) reads that input from dst; the

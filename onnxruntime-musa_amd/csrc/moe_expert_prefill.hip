@@ -90,7 +90,7 @@ struct PStage {
   int32_t ksplit;   // K splits (partial planes of the output)
   int32_t out_half; // fc2 with one plane: y2 stored in the activation type
   int32_t kstages;  // stages per K split
-  int32_t tiled;    // weights tile-major (int4 / int8), K padded to whole stages
+  int32_t tiled;    // weights tile-major (int4 / int8 / 16-bit), K padded to whole chunks of 128
   int32_t deint;    // fused interleaved fc1 stored de-interleaved (gate rows, then linear rows)
   int32_t stiled;   // block scales (block 32 / 64) tile-major, rows as the weights
   int64_t out_rows;
@@ -152,8 +152,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   // the scalar offset).  Rows of features past nfeat are read (past the
   // buffer: zeros) but their outputs are never stored. ----
   // bytes of one weight row (tile-major: K padded to whole stages of BK)
-  const bool tiled = WF != kDense && p.tiled != 0;
-  const int64_t rb = tiled ? static_cast<int64_t>((K + BK - 1) / BK) * BK * G::EBITS / 8
+  const bool tiled = p.tiled != 0;
+  const int64_t rb = tiled ? static_cast<int64_t>((K + 127) / 128) * 128 * G::EBITS / 8  // whole chunks of 128 k
                            : static_cast<int64_t>(K) * G::EBITS / 8;
   const uint8_t* wbase_g = p.w + static_cast<int64_t>(e) * p.w_rows * rb;
   const uint8_t* wbase_l = p.wl + static_cast<int64_t>(e) * p.wl_rows * rb;
@@ -178,18 +178,24 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   int64_t wdrow[kNT];
 #pragma unroll
   for (int j = 0; j < kNT; ++j) wdrow[j] = deint ? (j == 0 ? 0 : p.nfeat) : drow[j];
-  // Tile-major weights (pre-packed, int4 / int8; a stage is one chunk of
-  // 128 k): the 16 rows x 128 k of a weight tile and chunk are one block of
-  // CB bytes in which piece q (16 bytes) of row r sits at ((q % kv) * 64 + (q
-  // / kv) * 16 + r) * 16, kv = 16-byte vectors per 32 k.  Lane half h reads
-  // pieces BVEC h .. BVEC h + BVEC - 1 of its row.  wdrow steps (0, 32,
-  // nfeat) are whole tiles, so they stay row offsets.
-  constexpr int kKv = WF == kInt8 ? 2 : 1;
+  // Tile-major weights (pre-packed): the 16 rows x 128 k of a weight tile
+  // and chunk are one block of CB bytes in which piece q (16 bytes) of row r
+  // sits at ((q % kv) * 64 + (q / kv) * 16 + r) * 16, kv = 16-byte vectors
+  // per 32 k (1 int4, 2 int8, 4 16-bit).  A stage is one chunk (int4, int8)
+  // or half of one (16-bit, 64 k); lane half h reads the stage's 32-k groups
+  // from KH h / 32 on, BVEC pieces of its row.  wdrow steps (0, 32, nfeat)
+  // are whole tiles, so they stay row offsets.
+  constexpr int kKv = WF == kInt8 ? 2 : (WF == kDense ? 4 : 1);
   constexpr int CB = 1024 * kKv;
   const uint32_t woff =
-      tiled ? static_cast<uint32_t>((wrow0 / 16) * 16 * rb + (wrow0 % 16) * 16 + static_cast<int64_t>(kbeg / BK) * CB + 512 * h)
+      tiled ? static_cast<uint32_t>((wrow0 / 16) * 16 * rb + (wrow0 % 16) * 16 + (KH / 32) * 256 * h)
             : static_cast<uint32_t>(wrow0 * rb + static_cast<int64_t>(kbeg + KH * h) * G::EBITS / 8);
-  const int cstride = tiled ? CB : BK * G::EBITS / 8;  // weight bytes per stage
+  // bytes from woff to the lane's first piece of stage c
+  auto wstage = [&](int c) -> uint32_t {
+    if (!tiled) return static_cast<uint32_t>(c * BK * G::EBITS / 8);
+    const int k = kbeg + c * BK;  // a multiple of 64
+    return static_cast<uint32_t>((k / 128) * CB + ((k / 32) % 4) * 256);
+  };
   // offset of vector v beyond 16 v (tiled: piece BVEC h + v)
   int vdelta[BVEC];
 #pragma unroll
@@ -299,7 +305,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PStage p) {
   auto fetch = [&](int c, Ring& d) {
     const int k0 = kbeg + c * BK + KH * h;  // first k of the lane's range
     const bool kin = (c < nst) & (k0 < K);
-    const uint32_t o = kin ? woff + static_cast<uint32_t>(c * cstride) : kOob;
+    const uint32_t o = kin ? woff + wstage(c) : kOob;
 #pragma unroll
     for (int j = 0; j < kNT; ++j) {
       const __amdgpu_buffer_rsrc_t rw = GATED && j == 1 ? rs_l : rs_g;

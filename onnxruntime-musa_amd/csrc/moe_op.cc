@@ -124,9 +124,10 @@ struct moe_kernel {
   // begin and an end line per call to stderr; debug_sync waits for the
   // stream after each stage and turns a failure into MOE_EP_FAIL naming it
   bool trace = false, debug_sync = false;
-  // Pre-packed (tile-major) expert weights by QMoE input index (2 fc1, 5
-  // fc2, 8 fc3): the caller-owned device copy and the tensor it was packed
-  // from (shape, type and data pointer).
+  // Pre-packed (tile-major) expert weights by input index (QMoE: 2 fc1, 5
+  // fc2, 8 fc3 and 3, 6, 9 their block scales; MoE: 2 fc1, 4 fc2, 6 fc3):
+  // the caller-owned device copy and the tensor it was packed from (shape,
+  // type and data pointer).
   struct Packed {
     const void* data = nullptr;
     moe_tensor src{};
@@ -322,13 +323,25 @@ bool env_set(const char* name) {
   return v && *v && std::strcmp(v, "0") != 0;
 }
 
-// Bytes of the tile-major copy of QMoE weight input idx, or 0 when the
+// Input indices of the fc1 / fc2 / fc3 expert weights: QMoE 2, 5, 8; MoE
+// 2, 4, 6.
+int fc2_input(const moe_kernel* kr) { return kr->quantized ? 5 : 4; }
+int fc3_input(const moe_kernel* kr) { return kr->quantized ? 8 : 6; }
+
+// Bytes of one row's chunk of 128 k: int4 64, int8 128, 16-bit (MoE) 256.
+int64_t chunk_bytes(const moe_kernel* kr) {
+  if (!kr->quantized) return 256;
+  return kr->attrs.expert_weight_bits == 4 ? 64 : 128;
+}
+
+// Bytes of the tile-major copy of expert-weight input idx, or 0 when the
 // kernels read that input in the op's layout (see moe_prepack.hip).  A
 // weight is packed when each expert's rows are whole 16-row tiles (the
 // gate and linear halves of a fused fc1 each), rows are whole 16-byte
 // pieces (K is padded to whole chunks of 128 in the copy), and the kernels
-// that read it take tile-major weights: fp16/bf16 activations (MFMA paths);
-// fc1/fc3 with K within one decode activation slice.
+// that read it take tile-major weights: fp16/bf16 activations (MFMA paths,
+// MoE weights of the activations' type); fc1/fc3 with K within one decode
+// activation slice.
 // Bytes of the tile-major copy of QMoE block-scale input idx (3 fc1, 6
 // fc2, 9 fc3), or 0: scales are packed for the step-scale decode kernels
 // (block 32 or 64; int4, or int8 with fp16 activations) when their weights
@@ -358,13 +371,16 @@ size_t prepack_scale_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* 
 moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w, int32_t act_type,
                          size_t* bytes) {
   *bytes = 0;
-  const bool scales = idx == 3 || idx == 6 || idx == 9;
-  if (idx != 2 && idx != 5 && idx != 8 && !scales)
-    return fail(MOE_INVALID_ARGUMENT, "input_index must be 2, 5 or 8 (QMoE expert weights) or 3, 6 or 9 "
-                                      "(their scales), got " + std::to_string(idx));
+  const bool q = kr->quantized;
+  const bool scales = q && (idx == 3 || idx == 6 || idx == 9);
+  const bool weights = idx == 2 || idx == fc2_input(kr) || idx == fc3_input(kr);
+  if (!weights && !scales)
+    return fail(MOE_INVALID_ARGUMENT, q ? "input_index must be 2, 5 or 8 (QMoE expert weights) or 3, 6 or 9 "
+                                          "(their scales), got " + std::to_string(idx)
+                                        : "input_index must be 2, 4 or 6 (MoE expert weights), got " +
+                                              std::to_string(idx));
   if (!w || !w->data) return fail(MOE_INVALID_ARGUMENT, "null weights");
   if (!is_float_type(act_type)) return fail(MOE_INVALID_ARGUMENT, "act_type must be a float type");
-  if (!kr->quantized) return MOE_OK;
   if (scales) {
     // per output channel [E, N] (kept as given) or per block [E, N, K / block]
     if ((w->rank != 2 && w->rank != 3) || (!is_float_type(w->elem_type) && w->elem_type != MOE_ELEM_UINT8) ||
@@ -373,17 +389,20 @@ moe_status prepack_bytes(const moe_kernel* kr, int32_t idx, const moe_tensor* w,
     if (w->rank == 3) *bytes = prepack_scale_bytes(kr, idx, w, act_type);
     return MOE_OK;
   }
-  if (w->elem_type != MOE_ELEM_UINT8 || w->rank != 3 || w->dims[0] <= 0)
+  if (q && (w->elem_type != MOE_ELEM_UINT8 || w->rank != 3 || w->dims[0] <= 0))
     return fail(MOE_INVALID_ARGUMENT, "QMoE expert weights must be 3D uint8, got " + dims_str(*w));
+  if (!q && (!is_float_type(w->elem_type) || w->rank != 3 || w->dims[0] <= 0))
+    return fail(MOE_INVALID_ARGUMENT, "MoE expert weights must be 3D float, got " + dims_str(*w));
   if (act_type == MOE_ELEM_FLOAT) return MOE_OK;
+  if (!q && w->elem_type != act_type) return MOE_OK;  // the op rejects the call: nothing to pack for
   const moe_attributes& at = kr->attrs;
-  const int64_t cbytes = at.expert_weight_bits == 4 ? 64 : 128;
-  const int64_t E = w->dims[0], N = w->dims[1], rb = w->dims[2];
+  const int64_t cbytes = chunk_bytes(kr);
+  const int64_t E = w->dims[0], N = w->dims[1], rb = w->dims[2] * (q ? 1 : 2);  // bytes of a row
   const bool swiglu = at.activation_type == MOE_ACT_SWIGLU;
   if (N <= 0 || N % 16 || rb <= 0 || rb % 16) return MOE_OK;
   const int64_t rbp = (rb + cbytes - 1) / cbytes * cbytes;  // padded to whole chunks
   if (N * rbp >= (int64_t{1} << 31)) return MOE_OK;        // 32-bit buffer offsets per expert
-  if (idx != 5) {
+  if (idx != fc2_input(kr)) {
     if (rbp / cbytes * 128 > moe::kStreamMaxK) return MOE_OK;
     if (swiglu && (at.swiglu_fusion == 1 || at.swiglu_fusion == 2) && N % 32) return MOE_OK;
   }
@@ -426,8 +445,8 @@ moe::ExpertArgs expert_args(const moe_kernel* kr, const Problem& p, const Layout
   } else {
     a.b1 = d(3); a.w2 = d(4); a.b2 = d(5); a.w3 = d(6); a.b3 = d(7);
   }
-  a.tiled1 = q && kr->packed[2].data ? 1 : 0;
-  a.tiled2 = q && kr->packed[5].data ? 1 : 0;
+  a.tiled1 = kr->packed[2].data ? 1 : 0;
+  a.tiled2 = kr->packed[fc2_input(kr)].data ? 1 : 0;
   a.deint1 = a.tiled1 && kr->packed[2].deint ? 1 : 0;
   a.stiled1 = q && kr->packed[3].data ? 1 : 0;
   a.stiled2 = q && kr->packed[6].data ? 1 : 0;
@@ -563,9 +582,9 @@ moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe
       return fail(MOE_INVALID_ARGUMENT, "pre-pack buffer too small: need " + std::to_string(need) + " bytes");
     if (reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(weights->data) % 16)
       return fail(MOE_INVALID_ARGUMENT, "weights and pre-pack buffer must be 16-byte aligned");
-    const int cbytes = kernel->attrs.expert_weight_bits == 4 ? 64 : 128;
+    const int cbytes = static_cast<int>(chunk_bytes(kernel));
     const bool deint = prepack_deint(kernel, input_index);
-    const bool scales = input_index == 3 || input_index == 6 || input_index == 9;
+    const bool scales = kernel->quantized && (input_index == 3 || input_index == 6 || input_index == 9);
     const hipError_t e =
         scales ? moe::launch_prepack_scales(weights->data, dst,
                                             weights->elem_type == MOE_ELEM_FLOAT ? 4
@@ -574,7 +593,8 @@ moe_status moe_kernel_prepack(moe_kernel* kernel, int32_t input_index, const moe
                                             static_cast<int>(kernel->attrs.block_size), weights->dims[1], deint,
                                             static_cast<hipStream_t>(stream))
                : moe::launch_prepack(static_cast<const uint8_t*>(weights->data), static_cast<uint8_t*>(dst),
-                                     weights->dims[0] * weights->dims[1], weights->dims[2], cbytes, weights->dims[1],
+                                     weights->dims[0] * weights->dims[1],
+                                     weights->dims[2] * (kernel->quantized ? 1 : 2), cbytes, weights->dims[1],
                                      deint, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pre-pack launch");
     kernel->packed[input_index].data = dst;
@@ -735,9 +755,11 @@ moe_status compute_impl(const moe_kernel* kernel, const moe_tensor* inputs, int3
     }
     moe::ExpertArgs a = expert_args(kernel, p, l, ws, output);
     auto packed = [&](int i) { return kernel->packed[i].data != nullptr; };
-    if (p.gate_mode == moe::kGateFc3 && (packed(2) != packed(8) || packed(3) != packed(9)))
+    const bool q = kernel->quantized;
+    if (p.gate_mode == moe::kGateFc3 &&
+        (packed(2) != packed(fc3_input(kernel)) || (q && packed(3) != packed(9))))
       return fail(MOE_NOT_IMPLEMENTED, "fc1 and fc3 weights (and scales) must both be pre-packed or neither");
-    if ((packed(3) && !packed(2)) || (packed(6) && !packed(5)) || (packed(9) && !packed(8)))
+    if (q && ((packed(3) && !packed(2)) || (packed(6) && !packed(5)) || (packed(9) && !packed(8))))
       return fail(MOE_NOT_IMPLEMENTED, "pre-packed scales need their weights pre-packed");
     const int path = choose_path(kernel, a);
     if (path < 0)

@@ -1,10 +1,12 @@
-// moe_prepack.hip -- one-time reordering of QMoE expert weights into the
-// tile-major layout the decode and prefill kernels read.
+// moe_prepack.hip -- one-time reordering of expert weights (QMoE int4 /
+// int8, MoE fp16 / bf16) into the tile-major layout the decode and prefill
+// kernels read.
 //
 // The op's layout is row-major per expert: [E, N, K/pack] bytes, K
 // contiguous within an output row.  A decode wave's load instruction covers
-// 16 rows x 16 bytes per lane group, i.e. 16 separate 64-byte (int4) or
-// 128-byte (int8) runs of one chunk of 128 k.  Tile-major stores each
+// 16 rows x 16 bytes per lane group, i.e. 16 separate 64-byte (int4),
+// 128-byte (int8) or 256-byte (16-bit) runs of one chunk of 128 k, and a
+// prefill wave's 32 rows x 2 halves likewise.  Tile-major stores each
 // (16-row tile, chunk) as one contiguous block, so that the same instruction
 // reads 1 KB in one run:
 //
@@ -12,8 +14,8 @@
 //   piece q (16 bytes, k [32 q / kv .. ] of the chunk row) of row r inside
 //     it at ((q % kv) * 64 + (q / kv) * 16 + r) * 16
 //
-// with cbytes = 64 (int4) or 128 (int8) bytes of one row per chunk and kv =
-// cbytes / 64 16-byte vectors per 32 k.  Lane l = 16 g + r of a decode wave
+// with cbytes = 64 (int4), 128 (int8) or 256 (16-bit) bytes of one row per
+// chunk and kv = cbytes / 64 16-byte vectors per 32 k.  Lane l = 16 g + r of a decode wave
 // then reads piece kv g + v of row r at v * 1 KB + 16 l, and rows never
 // cross an expert (N is a multiple of 16), so the experts can be packed as
 // one [E * N, K/pack] matrix.
@@ -108,7 +110,8 @@ hipError_t launch_prepack_scales(const void* src, void* dst, int elem_bytes, int
 
 hipError_t launch_prepack(const uint8_t* src, uint8_t* dst, int64_t rows, int64_t row_bytes, int cbytes,
                           int64_t expert_rows, bool deint, hipStream_t stream) {
-  if (rows % 16 || row_bytes % 16 || (cbytes != 64 && cbytes != 128) || expert_rows <= 0 || rows % expert_rows ||
+  if (rows % 16 || row_bytes % 16 || (cbytes != 64 && cbytes != 128 && cbytes != 256) || expert_rows <= 0 ||
+      rows % expert_rows ||
       (deint && expert_rows % 32))
     return hipErrorInvalidValue;
   const int64_t nchunks = (row_bytes + cbytes - 1) / cbytes;

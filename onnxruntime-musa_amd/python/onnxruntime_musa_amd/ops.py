@@ -260,6 +260,8 @@ class MoE(_MoEOp):
     """com.microsoft MoE (float expert weights)."""
     op_type = "MoE"
     input_names = MOE_INPUTS
+    # fc1, fc2, fc3 expert weights (packed when fp16 / bf16, like the activations)
+    WEIGHT_INPUTS = (2, 4, 6)
 
 
 class QMoE(_MoEOp):

@@ -352,12 +352,52 @@ def test_prepack_size_chunked_fc1_needs_whole_tiles_per_half(lib):
         lib.moe_kernel_release(h)
 
 
-def test_prepack_size_fp32_activations_and_moe_stay_row_major(lib, qkernel):
+def test_prepack_size_fp32_activations_stay_row_major(lib, qkernel):
     assert prepack_size(lib, qkernel, 2, [8, 512, 128], act=C.ELEM_FLOAT) == (C.MOE_OK, 0)
     st, h = create(lib, "MoE", k=2, activation_type=2)
     assert st == C.MOE_OK
     try:
-        assert prepack_size(lib, h, 2, [8, 512, 256], et=C.ELEM_FLOAT16) == (C.MOE_OK, 0)
+        assert prepack_size(lib, h, 2, [8, 512, 256], act=C.ELEM_FLOAT, et=C.ELEM_FLOAT) == (C.MOE_OK, 0)
+    finally:
+        lib.moe_kernel_release(h)
+
+
+# MoE (16-bit weights of the activations' type): fc1 2, fc2 4, fc3 6; a
+# row's K padded to whole chunks of 128 k (256 bytes)
+@pytest.mark.parametrize("idx,dims,et,act,packed_rb", [
+    (2, [8, 512, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 512),
+    (4, [8, 256, 768], C.ELEM_BFLOAT16, C.ELEM_BFLOAT16, 1536),
+    (6, [8, 512, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 512),
+    (2, [8, 512, 320], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 768),     # K = 320: 2.5 chunks -> 3
+    (4, [8, 256, 8192], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 16384),  # fc2 K = 8192 streams in slices
+    (2, [8, 512, 8192], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 0),      # fc1 K above one decode slice
+    (2, [8, 520, 256], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 0),       # N not a multiple of 16
+    (2, [8, 512, 100], C.ELEM_FLOAT16, C.ELEM_FLOAT16, 0),       # rows not whole 16-byte pieces
+    (2, [8, 512, 256], C.ELEM_BFLOAT16, C.ELEM_FLOAT16, 0),      # not the activations' type
+])
+def test_prepack_size_moe(lib, idx, dims, et, act, packed_rb):
+    st, h = create(lib, "MoE", k=2, activation_type=4)
+    assert st == C.MOE_OK
+    try:
+        st, n = prepack_size(lib, h, idx, dims, act=act, et=et)
+        assert st == C.MOE_OK, lib.moe_last_error()
+        assert n == dims[0] * dims[1] * packed_rb
+    finally:
+        lib.moe_kernel_release(h)
+
+
+@pytest.mark.parametrize("idx,dims,et", [
+    (3, [8, 512], C.ELEM_FLOAT16),          # fc1 bias
+    (5, [8, 256, 512], C.ELEM_FLOAT16),     # fc2 bias index (QMoE's fc2 weights)
+    (8, [8, 256, 512], C.ELEM_FLOAT16),
+    (2, [8, 512, 256], C.ELEM_UINT8),       # not a float type
+    (2, [512, 256], C.ELEM_FLOAT16),        # not 3D
+])
+def test_prepack_moe_rejects_bad_arguments(lib, idx, dims, et):
+    st, h = create(lib, "MoE", k=2, activation_type=4)
+    assert st == C.MOE_OK
+    try:
+        assert prepack_size(lib, h, idx, dims, et=et)[0] == C.MOE_INVALID_ARGUMENT
     finally:
         lib.moe_kernel_release(h)
 

@@ -1,4 +1,5 @@
-"""Pre-packed (tile-major) QMoE expert weights on the GPU.
+"""Pre-packed (tile-major) expert weights on the GPU: QMoE int4 / int8 and
+MoE fp16 / bf16.
 
 The pack kernel's output is compared byte for byte with a numpy statement of
 the layout (onnxruntime-musa_amd/csrc/moe_prepack.hip).  The op reading
@@ -20,16 +21,21 @@ from onnxruntime_musa_amd.workloads import CONFIGS, make_problem, to_host
 pytestmark = pytest.mark.gpu
 
 C2, C3, C4 = CONFIGS["c2_qmoe_int8_mixtral"], CONFIGS["c3_qmoe_int4_mixtral"], CONFIGS["c4_qmoe_int4_gptoss"]
+C5 = CONFIGS["c5_moe_f16_qwen3"]
 
 
 def pack_reference(w: np.ndarray, bits: int, deint: bool = False) -> np.ndarray:
     """Tile-major layout: one block of 16 * cb bytes per (16-row tile, chunk
-    of 128 k), cb = 64 (int4) or 128 (int8) bytes of a row per chunk; the
-    16-byte piece q of row r of the tile sits at slot (q % kv) * 64 + (q //
-    kv) * 16 + r of the block, kv = cb / 64.  Rows are padded with zeros to
-    whole chunks; deint: each expert's rows 0, 2, 4, .. then 1, 3, 5, .."""
+    of 128 k), cb = 64 (int4), 128 (int8) or 256 (16-bit) bytes of a row per
+    chunk; the 16-byte piece q of row r of the tile sits at slot (q % kv) *
+    64 + (q // kv) * 16 + r of the block, kv = cb / 64.  Rows are padded with
+    zeros to whole chunks; deint: each expert's rows 0, 2, 4, .. then 1, 3,
+    5, .."""
+    w = np.ascontiguousarray(w)
+    if w.dtype != np.uint8:  # 16-bit weights: their bytes
+        w = w.view(np.uint8)
     E, N, rb = w.shape
-    cb = 64 if bits == 4 else 128
+    cb = {4: 64, 8: 128, 16: 256}[bits]
     kv, cp, nch = cb // 64, cb // 16, -(-rb // cb)
     if deint:
         w = np.concatenate([w[:, 0::2], w[:, 1::2]], axis=1)
@@ -66,6 +72,26 @@ def test_pack_layout_padded_and_deinterleaved(cuda, bits, idx):
     torch.cuda.synchronize()
     assert packed is not None
     np.testing.assert_array_equal(packed.cpu().numpy(), pack_reference(to_host(w), bits, deint=idx == 2))
+
+
+@pytest.mark.parametrize("dtype,over", [("f16", dict(hidden=256, inter=384)),
+                                        ("bf16", dict(hidden=320, inter=160, use_fc3=False, swiglu_fusion=1))],
+                         ids=["f16-fc3", "bf16-interleaved-k320"])
+@pytest.mark.parametrize("which", ["fc1", "fc2", "fc3"])
+def test_pack_layout_moe(cuda, dtype, over, which):
+    p = make_problem(replace(C5, dtype=dtype, experts=4, k=2, router="normal", **over), 4, seed=14, device=cuda,
+                     gen="numpy")
+    idx = {"fc1": 2, "fc2": 4, "fc3": 6}[which]
+    ins = p.schema_inputs()
+    w = ins[idx] if idx < len(ins) else None
+    if w is None:
+        pytest.skip("no fc3 weights (fused fc1)")
+    op = p.make_op()
+    packed = op.prepack(idx, w, w.dtype)
+    torch.cuda.synchronize()
+    assert packed is not None
+    deint = idx == 2 and p.cfg.swiglu_fusion == 1
+    np.testing.assert_array_equal(packed.cpu().numpy(), pack_reference(to_host(w), 16, deint=deint))
 
 
 def pack_scales_reference(s: np.ndarray, block: int, deint: bool = False) -> np.ndarray:
@@ -113,6 +139,12 @@ VARIANTS = {
     "int4-b32-f16": (C3, dict(hidden=256, inter=384, block_size=32)),
     "int8-b32-f16-deint": (C4, dict(hidden=320, inter=160, experts=8, bits=8, dtype="f16", scale_dtype="f16")),
     "int4-b64-bf16-odd-blocks": (C4, dict(hidden=320, inter=192, experts=8, block_size=64)),
+    # MoE fp16 / bf16 weights: 256-byte chunks, prefill stages of half a chunk
+    "f16-moe-fc3": (C5, dict(hidden=256, inter=384, experts=8, k=2, router="normal")),
+    "bf16-moe-interleaved-k320": (C5, dict(hidden=320, inter=160, experts=8, k=2, router="normal", dtype="bf16",
+                                           use_fc3=False, swiglu_fusion=1, bias=True)),
+    "f16-moe-silu-fc2-slices": (C5, dict(hidden=512, inter=8192, experts=4, k=2, router="normal", use_fc3=False,
+                                         activation="silu")),
 }
 
 
@@ -224,6 +256,12 @@ def test_fc1_and_fc3_pack_together(cuda):
 def test_full_decode_prepacked(cuda, name, T):
     p = make_problem(CONFIGS[name], T, seed=300 + T, device=cuda)
     check_problem(p, threads=16, prepack=True)
+
+
+@pytest.mark.parametrize("T", [16, 8192])
+def test_full_c5_prepacked(cuda, T):
+    p = make_problem(C5, T, seed=500 + T, device=cuda)
+    check_problem(p, sample_tokens=48 if T > 64 else None, threads=16, prepack=True, report=True)
 
 
 @pytest.mark.parametrize("name", ["c2_qmoe_int8_mixtral", "c3_qmoe_int4_mixtral"])
