@@ -316,7 +316,24 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // an expert with more rows streams its weights once per group.
   // exl[0 .. e_act) ----
   int e_act = 0;
-  for (int base = 0; base < E; base += NT) {
+  if (E <= kWave) {
+    // one wavefront: lane e's groups, then one barrier
+    if (wave == 0) {
+      const int cnt = lane < E ? offs[lane + 1] - offs[lane] : 0;
+      const int nv = (cnt + kStreamRows - 1) / kStreamRows;
+      int inc = nv;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int t = __shfl_up(inc, o, kWave);
+        if (lane >= o) inc += t;
+      }
+      for (int j = 0; j < nv; ++j) exl[inc - nv + j] = lane | (j << 16);
+      if (lane == kWave - 1) wcount[0] = inc;
+    }
+    __syncthreads();
+    e_act = wcount[0];
+  }
+  for (int base = 0; base < E && E > kWave; base += NT) {
     const int e = base + tid;
     const int cnt = e < E ? offs[e + 1] - offs[e] : 0;
     const int nv = (cnt + kStreamRows - 1) / kStreamRows;

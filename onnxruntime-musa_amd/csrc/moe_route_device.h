@@ -182,11 +182,83 @@ inline size_t route_block_scratch_bytes(int64_t T, int64_t E, int64_t k, int nwa
   return static_cast<size_t>((2 * E + nwaves * E + T * k) * 4 + T * E * logit_bytes);
 }
 
+// route_dispatch_block for at most 64 rows (T k) and 64 experts: the waves
+// route their tokens (logits read from global, each element once per
+// workgroup), then wavefront 0 alone counts, scans and ranks the rows, one
+// row per lane (rank = rows with a lower flat index and the same expert,
+// from a ballot-built match mask): two barriers in all, no atomics.  The
+// same results as the general path.
+template <typename LT>
+__device__ void route_dispatch_wave(const moe_route_params& p, int* offs, int* perm, int* scratch, bool publish) {
+  const int E = static_cast<int>(p.num_experts), k = static_cast<int>(p.k);
+  const int T = static_cast<int>(p.num_tokens), n = T * k;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int nwaves = blockDim.x / kWave;
+  int* ids = scratch;     // [n] expert of each row (flat index t k + j)
+  int* cnt = ids + n;     // [E] rows per expert
+  const int tpw = route_group_tokens(E);
+  for (int t0 = wave * tpw; t0 < T; t0 += nwaves * tpw) {
+    int64_t t;
+    int id;
+    float w;
+    if (route_group<LT>(p.logits, t0, T, E, k, p.normalize != 0, p.sigmoid != 0, lane, &t, &id, &w)) {
+      const int e = lane % (kWave / tpw);
+      ids[t * k + e] = id;
+      if (publish) {
+        p.topk_ids[t * k + e] = id;
+        p.topk_w[t * k + e] = w;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // a wavefront's LDS accesses complete in order, so each store below is
+    // seen by the loads after it; the accesses that read other lanes'
+    // stores are volatile, so that the compiler keeps them in order too
+    volatile int* vcnt = cnt;
+    volatile int* voffs = offs;
+    const bool act = lane < n;
+    const int ef = act ? ids[lane] : 0;
+    const uint64_t mm = match_mask(ef, act, id_bits(E));
+    const int r = lanes_below(mm, lane);
+    if (lane < E) vcnt[lane] = 0;
+    if (act && r == 0) vcnt[ef] = __popcll(mm);
+    const int c = lane < E ? vcnt[lane] : 0;
+    int inc = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int v = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += v;
+    }
+    if (lane < E) {
+      voffs[lane] = inc - c;
+      if (publish) p.offsets[lane] = inc - c;
+    }
+    if (lane == kWave - 1) {
+      voffs[E] = inc;
+      if (publish) p.offsets[E] = inc;
+    }
+    if (act) {
+      const int row = voffs[ef] + r;
+      perm[row] = lane;
+      if (publish) {
+        p.perm[row] = lane;
+        p.inv_perm[lane] = row;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 template <typename LT>
 __device__ void route_dispatch_block(const moe_route_params& p, int* offs, int* perm, int* scratch,
                                      bool publish) {
   const int E = static_cast<int>(p.num_experts), k = static_cast<int>(p.k);
   const int T = static_cast<int>(p.num_tokens), n = T * k;
+  if (n <= kWave && E <= kWave) {
+    route_dispatch_wave<LT>(p, offs, perm, scratch, publish);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int nwaves = blockDim.x / kWave;
   int* cnt = scratch;
