@@ -283,6 +283,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   constexpr int kEs = static_cast<int>(sizeof(typename ST::storage));
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int wcount[NW];
+  __shared__ int loffs[kWave + 1];  // up to 64 experts: the offsets, read once
   const Stage& p = ss.s;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -317,9 +318,14 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // exl[0 .. e_act) ----
   int e_act = 0;
   if (E <= kWave) {
-    // one wavefront: lane e's groups, then one barrier
+    // one wavefront: lane e's groups, then one barrier.  The offsets it
+    // reads stay in LDS for the group loop (one global round trip less
+    // before the first loads when they come from the router kernels).
     if (wave == 0) {
-      const int cnt = lane < E ? offs[lane + 1] - offs[lane] : 0;
+      const int lo = lane < E ? offs[lane] : 0, hi = lane < E ? offs[lane + 1] : 0;
+      if (lane < E) loffs[lane] = lo;
+      if (lane == E - 1) loffs[E] = hi;
+      const int cnt = hi - lo;
       const int nv = (cnt + kStreamRows - 1) / kStreamRows;
       int inc = nv;
 #pragma unroll
@@ -332,6 +338,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     }
     __syncthreads();
     e_act = wcount[0];
+    offs = loffs;
   }
   for (int base = 0; base < E && E > kWave; base += NT) {
     const int e = base + tid;
