@@ -316,7 +316,42 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   // ---- row groups: each routed expert's rows in groups of 16 (the MFMA M);
   // an expert with more rows streams its weights once per group.
   // exl[0 .. e_act) ----
-  int e_act = 0;
+  //
+  // This workgroup's tiles [t_beg, t_end) follow from e_act (split below).
+  // Tiles of group q (row group a = q / nsl, slice s = q % nsl) are
+  // [q nft, (q + 1) nft).  Each group a workgroup touches costs a staging
+  // and a split-tile reduction, about kGroupCost tiles of streaming.  With
+  // fewer groups than workgroups, each group gets a whole number of
+  // workgroups (group q: workgroups i with i G / P == q) when the largest
+  // share that leaves is cheaper than an even split of all tiles plus the
+  // second group that the workgroups on a group boundary then pay.  All
+  // values are non-negative and tile counts stay far below 2^31 (row
+  // groups x slices x feature tiles), so the arithmetic is 32-bit unsigned.
+  // The scalar unit a CU's waves share would run it once per wave, so fc2,
+  // in the one-wave case, has wave 0 alone compute it and pass it on in
+  // LDS (fc1 keeps it in every wave: measured no gain there, and a loss at
+  // gpt-oss int4).
+  constexpr int kGroupCost = 2;
+  const uint32_t P = gridDim.x, bx = blockIdx.x;
+  const int nft = static_cast<int>((p.nfeat + 16 * FT - 1) / (16 * FT));
+  auto split = [&](uint32_t ngq, int* tb, int* te) {
+    const uint32_t nf = static_cast<uint32_t>(nft), ttot = ngq * nf;
+    if (ngq == 0) {
+      *tb = *te = 0;
+    } else if (ngq <= P && (nf + P / ngq - 1) / (P / ngq) < kGroupCost + (ttot + P - 1) / P) {
+      const uint32_t q = bx * ngq / P;
+      const uint32_t w0 = (q * P + ngq - 1) / ngq, nw = ((q + 1) * P + ngq - 1) / ngq - w0;
+      const uint32_t j = bx - w0;
+      *tb = static_cast<int>(q * nf + nf * j / nw);
+      *te = static_cast<int>(q * nf + nf * (j + 1) / nw);
+    } else {
+      // floor(ttot * b / P) without a 64-bit product
+      const uint32_t qt = ttot / P, rt = ttot % P;
+      *tb = static_cast<int>(qt * bx + rt * bx / P);
+      *te = static_cast<int>(qt * (bx + 1) + rt * (bx + 1) / P);
+    }
+  };
+  int e_act = 0, t_beg = 0, t_end = 0;
   if (E <= kWave) {
     // one wavefront: lane e's groups, then one barrier.  The offsets it
     // reads stay in LDS for the group loop (one global round trip less
@@ -334,10 +369,18 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
         if (lane >= o) inc += t;
       }
       for (int j = 0; j < nv; ++j) exl[inc - nv + j] = lane | (j << 16);
-      if (lane == kWave - 1) wcount[0] = inc;
+      int tb = 0, te = 0;
+      if constexpr (!FC1) split(static_cast<uint32_t>(__builtin_amdgcn_readlane(inc, kWave - 1) * nsl), &tb, &te);
+      if (lane == kWave - 1) {
+        wcount[0] = inc;
+        wcount[1] = tb;
+        wcount[2] = te;
+      }
     }
     __syncthreads();
     e_act = wcount[0];
+    t_beg = wcount[1];
+    t_end = wcount[2];
     offs = loffs;
   }
   for (int base = 0; base < E && E > kWave; base += NT) {
@@ -364,6 +407,9 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
     __syncthreads();
   }
   e_act = __builtin_amdgcn_readfirstlane(e_act);
+  if (FC1 || E > kWave) split(static_cast<uint32_t>(e_act * nsl), &t_beg, &t_end);
+  t_beg = __builtin_amdgcn_readfirstlane(t_beg);
+  t_end = __builtin_amdgcn_readfirstlane(t_end);
 
   // ---- this workgroup's tiles ----
   const int64_t K = p.K;
@@ -374,33 +420,7 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   const bool tiled = STREAM_NT || p.tiled != 0;
   const uint32_t rb = tiled ? static_cast<uint32_t>(nchunks * 4 * LB)
                             : static_cast<uint32_t>((K / 32) * LB);  // bytes of one weight row
-  const int nft =static_cast<int>((p.nfeat + 16 * FT - 1) / (16 * FT));
-  // tile counts stay far below 2^31 (row groups x slices x feature tiles),
-  // so the partition and the group loop use 32-bit arithmetic
   const int per_a = nsl * nft;
-  const int ttot = e_act * per_a;
-  // Tiles of group q (row group a = q / nsl, slice s = q % nsl) are
-  // [q nft, (q + 1) nft).  Each group a workgroup touches costs a staging
-  // and a split-tile reduction, about kGroupCost tiles of streaming.  With
-  // fewer groups than workgroups, each group gets a whole number of
-  // workgroups (group q: workgroups i with i G / P == q) when the largest
-  // share that leaves is cheaper than an even split of all tiles plus the
-  // second group that the workgroups on a group boundary then pay.
-  constexpr int kGroupCost = 2;
-  const int ngq = e_act * nsl, P = static_cast<int>(gridDim.x), bx = static_cast<int>(blockIdx.x);
-  int t_beg, t_end;
-  if (ngq <= P && (nft + P / ngq - 1) / (P / ngq) < kGroupCost + (ttot + P - 1) / P) {
-    const int q = bx * ngq / P;
-    const int w0 = (q * P + ngq - 1) / ngq, nw = ((q + 1) * P + ngq - 1) / ngq - w0;
-    const int j = bx - w0;
-    t_beg = q * nft + nft * j / nw;
-    t_end = q * nft + nft * (j + 1) / nw;
-  } else {
-    // floor(ttot * b / P) without a 64-bit product
-    const int qt = ttot / P, rt = ttot % P;
-    t_beg = qt * bx + rt * bx / P;
-    t_end = qt * (bx + 1) + rt * (bx + 1) / P;
-  }
   const int bpt = ksc / PD;  // blocks per tile
   int bshift = 0;
   uint32_t nblk = 0;
@@ -462,9 +482,9 @@ __global__ void __launch_bounds__((SGeo<WF, GATED>::NW * 64), 1) gemv_stream_ker
   }
 
   for (int t = t_beg; t < t_end;) {
-    const int a = t / per_a;
+    const int a = static_cast<int>(static_cast<uint32_t>(t) / static_cast<uint32_t>(per_a));
     const int rem = t - a * per_a;
-    const int s = rem / nft, f0 = rem - s * nft;
+    const int s = static_cast<int>(static_cast<uint32_t>(rem) / static_cast<uint32_t>(nft)), f0 = rem - s * nft;
     const int ntl = t_end - t < nft - f0 ? t_end - t : nft - f0;
     const int nb = ntl * bpt;
     const int b0 = nb * wave / NW, b1 = nb * (wave + 1) / NW;
