@@ -728,9 +728,10 @@ hipError_t launch_fc2_prefill(const ExpertArgs& a, int* y2_planes, int* y2_half,
   st.stiled = a.stiled2;
   const int32_t splits = prefill_fc2_splits(a.T, a.H, a.I, a.E, a.k, a.wfmt);
   plan_grid(st, a.T, a.k, a.E, a.wfmt, a.H, splits);
-  // fp16 and one plane: y2 goes out in fp16 (one rounding of the expert
-  // output before the fp32 weighted sum; half the bytes written and read)
-  st.out_half = splits == 1 && a.act_type == MOE_ELEM_FLOAT16 ? 1 : 0;
+  // 16-bit activations and one plane: y2 goes out in the activation type
+  // (one rounding of the expert output before the fp32 weighted sum; half
+  // the bytes written and read)
+  st.out_half = splits == 1 && (a.act_type == MOE_ELEM_FLOAT16 || a.act_type == MOE_ELEM_BFLOAT16) ? 1 : 0;
   *y2_planes = splits;
   *y2_half = st.out_half;
   return launch_stage<false>(st, a, false, stream);

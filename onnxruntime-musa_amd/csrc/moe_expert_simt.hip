@@ -113,20 +113,14 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   const int64_t h0 = (static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x) * 4;
   if (h0 >= a.H) return;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.y2_half) {  // one fp16 plane
-    const _Float16* y2h = reinterpret_cast<const _Float16*>(a.y2);
+  if (a.y2_half) {  // one plane in the output type (fp16 or bf16)
+    using YS = typename OT::storage;
+    const YS* y2h = reinterpret_cast<const YS*>(a.y2);
     for (int64_t j = 0; j < a.k; ++j) {
       const int64_t f = t * a.k + j;
       const float w = a.topk_w[f];
-      const _Float16* y = y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H;
-      if (h0 + 4 <= a.H && (a.H % 4) == 0) {  // 8-byte aligned: one load of 4 values
-        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-        const half4_t v = *reinterpret_cast<const half4_t*>(y + h0);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += w * static_cast<float>(v[c]);
-      } else {
-        for (int c = 0; c < 4 && h0 + c < a.H; ++c) acc[c] += w * static_cast<float>(y[h0 + c]);
-      }
+      const YS* y = y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H;
+      for (int c = 0; c < 4 && h0 + c < a.H; ++c) acc[c] += w * to_f32<OT>(y[h0 + c]);
     }
     typename OT::storage* out = static_cast<typename OT::storage*>(a.out);
     for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
@@ -203,26 +197,31 @@ __global__ void __launch_bounds__(256) finalize_kernel(ExpertArgs a) {
   for (int c = 0; c < 4 && h0 + c < a.H; ++c) out[t * a.H + h0 + c] = from_f32<OT>(acc[c]);
 }
 
-// One fp16 plane (fp16 prefill without a K split), H a multiple of 8: one
-// thread per (token, 8 features), 16-byte loads and stores, the same sums in
-// the same order as finalize_kernel.
+// One plane in the output type (16-bit prefill without a K split), H a
+// multiple of 8: one thread per (token, 8 features), 16-byte loads and
+// stores, the same sums in the same order as finalize_kernel.
+template <typename OT>
 __global__ void __launch_bounds__(256) finalize_half8_kernel(ExpertArgs a) {
+  using YS = typename OT::storage;
   const int64_t t = blockIdx.x;
   const int64_t h0 = (static_cast<int64_t>(blockIdx.y) * blockDim.x + threadIdx.x) * 8;
   if (h0 >= a.H) return;
-  const _Float16* y2h = reinterpret_cast<const _Float16*>(a.y2);
+  const YS* y2h = reinterpret_cast<const YS*>(a.y2);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int64_t j = 0; j < a.k; ++j) {
     const int64_t f = t * a.k + j;
     const float w = a.topk_w[f];
-    const half8_t v = *reinterpret_cast<const half8_t*>(y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H + h0);
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(y2h + static_cast<int64_t>(a.inv_perm[f]) * a.H + h0);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] += w * static_cast<float>(v[c]);
+    for (int c = 0; c < 8; ++c)
+      acc[c] += w * to_f32<OT>(__builtin_bit_cast(YS, static_cast<uint16_t>(v[c / 2] >> (16 * (c % 2)))));
   }
-  half8_t o;
+  u32x4_t o;
 #pragma unroll
-  for (int c = 0; c < 8; ++c) o[c] = static_cast<_Float16>(acc[c]);
-  *reinterpret_cast<half8_t*>(static_cast<_Float16*>(a.out) + t * a.H + h0) = o;
+  for (int c = 0; c < 4; ++c)
+    o[c] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<OT>(acc[2 * c]))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<OT>(acc[2 * c + 1]))) << 16);
+  *reinterpret_cast<u32x4_t*>(static_cast<YS*>(a.out) + t * a.H + h0) = o;
 }
 
 }  // namespace
@@ -245,9 +244,10 @@ hipError_t launch_fc2_simt(const ExpertArgs& a, hipStream_t stream) {
 
 hipError_t launch_finalize(const ExpertArgs& a, hipStream_t stream) {
   if (a.T == 0) return hipSuccess;
-  if (a.y2_half && a.act_type == MOE_ELEM_FLOAT16 && a.H % 8 == 0) {
+  if (a.y2_half && (a.act_type == MOE_ELEM_FLOAT16 || a.act_type == MOE_ELEM_BFLOAT16) && a.H % 8 == 0) {
     const dim3 grid8(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + 2047) / 2048));
-    hipLaunchKernelGGL(finalize_half8_kernel, grid8, dim3(256), 0, stream, a);
+    if (a.act_type == MOE_ELEM_FLOAT16) hipLaunchKernelGGL(finalize_half8_kernel<F16>, grid8, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(finalize_half8_kernel<BF16>, grid8, dim3(256), 0, stream, a);
     return hipGetLastError();
   }
   dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((a.H + 1023) / 1024));

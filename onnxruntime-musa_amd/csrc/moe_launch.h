@@ -92,7 +92,7 @@ struct ExpertArgs {
   void* act;   // [T*k, I] in act_type
   float* y2;   // [y2_planes][T*k, H] fp32 (partial sums when split over K)
   int32_t y2_planes;
-  int32_t y2_half;  // 1: y2 is one plane of fp16 values (fp16 prefill without a K split)
+  int32_t y2_half;  // 1: y2 is one plane in the activation type (16-bit prefill without a K split)
   void* out;   // [T, H] act_type
 };
 
