@@ -209,7 +209,8 @@ MOE_API moe_status moe_kernel_compute_noalloc(const moe_kernel *kernel, const mo
  * of the stage intermediates: act[T*k, I] (fc1/fc3 + activation output, input
  * type, rows in dispatch order) and y2[y2_planes_max][T*k, H] (fp32 fc2
  * partial sums over K ranges, bias in plane 0, rows in dispatch order; planes
- * a call does not use are left untouched).
+ * a call does not use are left untouched; a 16-bit prefill call without a K
+ * split writes one plane of the input type there instead).
  * Library extension for parity tests; no reference counterpart. */
 typedef struct moe_workspace_layout {
   size_t topk_ids, topk_w, offsets, perm, inv_perm, total;
