@@ -623,6 +623,7 @@ void plan_grid(PStage& st, int64_t T, int64_t k, int64_t E, int wfmt, int64_t nr
       st.gn = g;
     }
   }
+  if (st.ntiles == 1) st.gn = 1;  // one weight tile (N <= 256): no padding slots
   st.ngroups = (st.ntiles + st.gn - 1) / st.gn;
   const int64_t bk = bk_for(wfmt);
   const int64_t stages = (st.K + bk - 1) / bk;
